@@ -1,0 +1,289 @@
+#!/usr/bin/env python3
+"""Benchmark of the BDH recurrent-attention forward path on one MI355X.
+
+Headline (``value``): chunked prefill of one BDH layer, BASELINE config 2:
+B=8, nh=4, T=512, N=8192, D=256, chunk 128, bf16 inputs / fp32 accumulate,
+RoPE (theta 65536) fused, tokens/s = B*T / step time.  A step is one call of
+the RoPE-fused recurrent forward over the whole batch (inputs resident in HBM).
+
+Also reported (``decode``): BASELINE config 3, 256 decode steps of B=64
+streams after a 1024-token prefill, fp32 rho, tokens/s = B / step time, with
+its HBM roofline.
+
+Roofline (algorithmic work):
+  prefill FLOP/step = B*nh*T*(4*N*D + (C-1)*(N+D))          vs 2.5 PFLOP/s bf16
+  decode  bytes/step = sum_streams (4N + 4D + 2*|A|*4D + 4D)  vs 8 TB/s HBM
+with |A| the exact active-row count of each stream at that step.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+METRIC = "prefill & decode tokens/s per BDH layer (D=256,n=32K); % MFMA / HBM roofline"
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+SEED = 20260729
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20, help="timed prefill steps")
+    ap.add_argument("--warmup", type=int, default=3, help="untimed prefill steps")
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--decode-warmup", type=int, default=4)
+    ap.add_argument("--decode-prefill", type=int, default=1024, help="tokens prefilled into rho")
+    ap.add_argument("--only", choices=("all", "prefill", "decode"), default="all")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline wall time")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------------------- #
+def lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho):
+    from burn_dragon_amd import _lib
+    st = lib.bdh_recurrent_attention_rope_fwd(
+        ctypes.byref(plan), _lib.BDH_BF16, ctypes.c_void_p(x.data_ptr()),
+        ctypes.c_void_p(v.data_ptr()), None, None, ctypes.byref(rope),
+        ctypes.c_void_p(ctx.data_ptr()), ctypes.c_void_p(rho.data_ptr()), 128,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    if st != 0:
+        raise RuntimeError(f"prefill failed: {_lib.last_error()}")
+
+
+def bench_prefill(torch, args):
+    from burn_dragon_amd import _lib
+    B, H, T, N, D, C = 8, 4, 512, 8192, 256, 128
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(SEED + 2)
+    x = torch.relu(torch.randn(B, H, T, N, generator=g, device=dev) - 1.645).to(torch.bfloat16)
+    v = (torch.randn(B, 1, T, D, generator=g, device=dev) / 16).to(torch.bfloat16)
+    ctx = torch.empty(B, H, T, D, device=dev, dtype=torch.float32)
+    rho = torch.empty(B, H, N, D, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    plan = _lib.BdhRecurrentPlan(B, H, 1, T, N, D)
+    rope = _lib.BdhRope(_lib.BDH_ROPE_SEQUENTIAL, 0, 0, 65536.0)
+    for _ in range(args.warmup):
+        lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record()
+        lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho)
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
+    flop = B * H * T * (4 * N * D + (C - 1) * (N + D))
+    ms = wall * 1e3 / args.steps
+    achieved = flop / (ev_ms * 1e-3) / 1e12
+    print(f"[prefill] {ms:.3f} ms/step wall, {ev_ms:.3f} ms/step events, "
+          f"{B * T / (ms * 1e-3) / 1e6:.2f} M tok/s, {achieved:.1f} TFLOP/s", flush=True)
+    return {
+        "ms_per_step": ms, "event_ms": ev_ms, "tokens_per_s": B * T / (ms * 1e-3),
+        "flop": flop,
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None,
+                     "kernel": "prefill pass: gram_bf16 + ctx_bf16 + state_bf16 (+ rope table, V transpose)",
+                     "flop_per_launch": flop},
+        "shape": {"B": B, "nh": H, "T": T, "N": N, "D": D, "chunk": C},
+    }
+
+
+def bench_decode(torch, args):
+    import burn_dragon_amd as bd
+    from burn_dragon_amd import _lib, rope as rp
+    B, H, N, D = 64, 4, 8192, 256
+    P = args.decode_prefill
+    K = args.decode_steps
+    W = args.decode_warmup
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(SEED + 3)
+    # rho pre-filled by a P-token synthetic prefill (untimed), bf16 MFMA path.
+    rho = torch.empty(B, H, N, D, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    step_b = 16
+    for b0 in range(0, B, step_b):
+        xp = torch.relu(torch.randn(step_b, H, P, N, generator=g, device=dev) - 1.645).to(torch.bfloat16)
+        vp = (torch.randn(step_b, 1, P, D, generator=g, device=dev) / 16).to(torch.bfloat16)
+        ctxp = torch.empty(step_b, H, P, D, device=dev, dtype=torch.float32)
+        plan = _lib.BdhRecurrentPlan(step_b, H, 1, P, N, D)
+        rope = _lib.BdhRope(_lib.BDH_ROPE_SEQUENTIAL, 0, 0, 65536.0)
+        lib_fwd_call(torch, lib, plan, xp, vp, rope, ctxp, rho[b0:b0 + step_b])
+        del xp, vp, ctxp
+    torch.cuda.synchronize()
+    xs = torch.relu(torch.randn(W + K, B, H, N, generator=g, device=dev) - 1.645)
+    vs = torch.randn(W + K, B, 1, D, generator=g, device=dev) / 16
+    a = torch.empty(B, H, D, device=dev, dtype=torch.float32)
+    rope = _lib.BdhRope(_lib.BDH_ROPE_SEQUENTIAL, 0, 0, 65536.0)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step(i):
+        rope.pos0 = P + i
+        st = lib.bdh_decode_step(B, H, 1, N, D, ctypes.c_void_p(xs[i].data_ptr()),
+                                 ctypes.c_void_p(vs[i].data_ptr()), ctypes.c_void_p(rho.data_ptr()),
+                                 ctypes.byref(rope), ctypes.c_void_p(a.data_ptr()), None, None, stream)
+        if st != 0:
+            raise RuntimeError(f"decode failed: {_lib.last_error()}")
+
+    for i in range(W):
+        step(i)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(K):
+        starts[k].record()
+        step(W + k)
+        ends[k].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    ev_ms = sum(ev) / K
+    # exact active rows per step -> algorithmic bytes
+    freqs = torch.from_numpy(rp.rope_freqs(N)).to(dev)
+    active = 0
+    for k in range(K):
+        active += int(rp.active_rows_mask(xs[W + k], P + W + k, freqs).sum().item())
+    S = B * H
+    bytes_total = K * S * (4 * N + 4 * D + 4 * D) + active * 2 * 4 * D
+    bytes_per_step = bytes_total / K
+    achieved = bytes_per_step / (ev_ms * 1e-3) / 1e9
+    ms = wall * 1e3 / K
+    frac_active = active / (K * S * N)
+    print(f"[decode] {ms:.4f} ms/step wall, {ev_ms:.4f} ms/step events, "
+          f"{B / (ms * 1e-3) / 1e6:.3f} M tok/s, {achieved:.0f} GB/s, active {frac_active:.4f}",
+          flush=True)
+    del xs, vs, rho
+    return {
+        "value": B / (ms * 1e-3), "unit": "tokens/s", "steps": K, "warmup": W,
+        "ms_per_step": ms, "event_ms": ev_ms,
+        "config": {"workload": "C3 decode, one BDH layer: B64 nh4 N8192 D256, fp32 rho "
+                   f"[64,4,8192,256] prefilled by {P} tokens, {K} steps, RoPE at the step position"},
+        "active_fraction": round(frac_active, 5),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "decode_kernel", "bytes_per_launch": round(bytes_per_step)},
+    }
+
+
+# --------------------------------------------------------------------------- #
+def cpu_baseline_prefill(target_s: float):
+    """Reference CPU path restated (oracle, test infrastructure): RoPE in the
+    reference's f32 op order, then the NdArray recurrence op sequence with
+    [N, D] temporaries, fp32, OpenMP over the 32 (b, h) streams, on a sample of
+    the C2 workload's first tokens."""
+    import numpy as np
+    from oracle import oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    B, H, N, D = 8, 4, 8192, 256
+    rng = np.random.default_rng(SEED + 2)
+    T = 4
+    secs = 0.0
+    while True:
+        x = np.maximum(rng.standard_normal((B, H, T, N), dtype=np.float32) - np.float32(1.645), 0)
+        v = (rng.standard_normal((B, 1, T, D), dtype=np.float32) / np.float32(16)).astype(np.float32)
+        t0 = time.perf_counter()
+        q = O.rope_rotate(x, pos0=0)
+        _, _, rec = O.ndarray_recurrent_f32(q, v, threads=threads)
+        secs = time.perf_counter() - t0
+        if secs >= target_s / 4 or T >= 512:
+            break
+        T = min(512, T * 4)
+    return {"value": round(B * T / secs, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"C2 shapes (B8 nh4 N8192 D256), first {T} tokens, fp32, RoPE + NdArray "
+                      f"op-sequence recurrence (linear.rs:43-57) in C, {secs:.2f} s wall"}
+
+
+def cpu_baseline_decode(target_s: float):
+    import numpy as np
+    from oracle import oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    B, H, N, D = 4, 4, 8192, 256
+    rng = np.random.default_rng(SEED + 3)
+    rho = (rng.standard_normal((B, H, N, D), dtype=np.float32) * np.float32(0.05)).astype(np.float32)
+    steps = 0
+    t_total = 0.0
+    while t_total < target_s / 2 and steps < 64:
+        x = np.maximum(rng.standard_normal((B, H, 1, N), dtype=np.float32) - np.float32(1.645), 0)
+        v = (rng.standard_normal((B, 1, 1, D), dtype=np.float32) / np.float32(16)).astype(np.float32)
+        t0 = time.perf_counter()
+        q = O.rope_rotate(x, pos0=1024 + steps)
+        _, rho, _ = O.ndarray_recurrent_f32(q, v, rho, threads=threads)
+        t_total += time.perf_counter() - t0
+        steps += 1
+    return {"value": round(B * steps / t_total, 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"C3 shapes with B={B} (16 streams), {steps} steps, fp32, RoPE + NdArray "
+                      f"op-sequence step over all N*D of rho, {t_total:.2f} s wall"}
+
+
+# --------------------------------------------------------------------------- #
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build runs the recurrent-attention path on a "
+              "single MI355X (streams shard across GPUs with no exchange; see DESIGN.md). "
+              "Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    import burn_dragon_amd as bd
+    if not bd.supports_backend():
+        print("device is not gfx950", file=sys.stderr)
+        sys.exit(2)
+
+    pre = bench_prefill(torch, args) if args.only in ("all", "prefill") else None
+    dec = bench_decode(torch, args) if args.only in ("all", "decode") else None
+
+    cpu_pre = cpu_dec = None
+    if not args.no_cpu_baseline:
+        if pre is not None:
+            cpu_pre = cpu_baseline_prefill(args.cpu_seconds)
+            print(f"[cpu] prefill {cpu_pre['value']} tokens/s on {cpu_pre['cores']} threads",
+                  flush=True)
+        if dec is not None:
+            cpu_dec = cpu_baseline_decode(args.cpu_seconds)
+            print(f"[cpu] decode {cpu_dec['value']} tokens/s on {cpu_dec['cores']} threads",
+                  flush=True)
+
+    if pre is not None:
+        out = {
+            "metric": METRIC, "value": round(pre["tokens_per_s"], 1), "unit": "tokens/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(pre["ms_per_step"], 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "C2 chunked prefill, one BDH layer: B8 nh4 T512 N8192 D256, "
+                                   "chunk 128, bf16 in / fp32 acc, RoPE fused, rho out fp32",
+                       "global_batch": 8, "seq_len": 512, "parallelism": "single-gpu"},
+            "roofline": pre["roofline"],
+            "cpu_baseline": cpu_pre,
+        }
+        if dec is not None:
+            dec["cpu_baseline"] = cpu_dec
+            out["decode"] = dec
+    else:
+        out = {"metric": METRIC, "value": round(dec["value"], 1), "unit": "tokens/s", "n_gpus": 1,
+               "steps": dec["steps"], "warmup": dec["warmup"],
+               "ms_per_step": round(dec["ms_per_step"], 5), "higher_is_better": True,
+               "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+               "config": dec["config"], "roofline": dec["roofline"], "cpu_baseline": cpu_dec}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,19 @@
+"""burn_dragon_amd: MI355X (gfx950) HIP implementation of burn_dragon's
+recurrent linear-attention forward path (chunked bf16-MFMA prefill with fused
+RoPE, sparse bandwidth-bound decode), behind the reference's custom-op
+surface.  The compute lives in libbdh_hip.so (C ABI: include/bdh_hip.h)."""
+from .recurrent import (CompiledRecurrentAttentionPlan, KernelProfileSnapshot,  # noqa: F401
+                        RecurrentAttentionOutput, RecurrentProfileSnapshot,
+                        recurrent_profile_enable, recurrent_profile_reset,
+                        recurrent_profile_snapshot, supports_backend,
+                        supports_recurrent_backend, try_fused_recurrent_attention,
+                        try_fused_recurrent_attention_rope,
+                        try_fused_recurrent_attention_wgpu,
+                        try_fused_recurrent_attention_wgpu_with_plan,
+                        try_fused_recurrent_attention_with_plan)
+from .attention import (CompiledDenseCausalAttentionPlan,  # noqa: F401
+                        supports_dense_causal_attention_backend,
+                        try_fused_dense_causal_attention,
+                        try_fused_dense_causal_attention_wgpu,
+                        try_fused_dense_causal_attention_with_plan)
+from .decode import DecodeOutput, decode_step  # noqa: F401

@@ -1,0 +1,353 @@
+// C ABI of libbdh_hip (declared in include/bdh_hip.h): argument validation
+// with the reference's None semantics, path selection, per-device scratch,
+// the RoPE frequency table and the profiling counters.
+#include <math.h>
+#include <string.h>
+
+#include <chrono>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "bdh_internal.h"
+
+namespace bdh {
+
+// ---------------------------------------------------------------- errors ----
+static thread_local std::string g_last_error;
+
+bdh_status fail(bdh_status st, const std::string& msg) {
+  g_last_error = msg;
+  return st;
+}
+
+bdh_status hip_fail(hipError_t e, const char* what) {
+  return fail(BDH_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// --------------------------------------------------------------- scratch ----
+namespace {
+struct DeviceScratch {
+  void* ptr[SLOT_COUNT] = {};
+  size_t bytes[SLOT_COUNT] = {};
+  std::map<std::pair<int64_t, uint32_t>, float*> freqs;
+};
+std::mutex g_scratch_mu;
+std::map<int, DeviceScratch> g_scratch;
+
+DeviceScratch& device_scratch(int dev) { return g_scratch[dev]; }
+}  // namespace
+
+bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc) {
+  int dev = 0;
+  BDH_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  DeviceScratch& ds = device_scratch(dev);
+  if (bytes == 0) bytes = 256;
+  if (ds.bytes[slot] < bytes) {
+    if (ds.ptr[slot]) {
+      // Work already queued may still use the old buffer.
+      BDH_HIP_TRY(hipDeviceSynchronize());
+      BDH_HIP_TRY(hipFree(ds.ptr[slot]));
+      ds.ptr[slot] = nullptr;
+      ds.bytes[slot] = 0;
+    }
+    const size_t grow = bytes + bytes / 4;
+    void* p = nullptr;
+    BDH_HIP_TRY(hipMalloc(&p, grow));
+    if (zero_on_alloc) BDH_HIP_TRY(hipMemset(p, 0, grow));
+    ds.ptr[slot] = p;
+    ds.bytes[slot] = grow;
+  }
+  *out = ds.ptr[slot];
+  return BDH_OK;
+}
+
+// ------------------------------------------------------------------ RoPE ----
+// Attention::build_freqs, Rope arm (attention.rs:559-563), in f32:
+//   exponent = (floor(idx / 2) * 2) / latent ; f = 1 / theta^exponent / (2 pi)
+void rope_freqs_host(int64_t latent, float theta, float* out) {
+  const float two_pi = 2.0f * 3.14159265358979323846f;
+  for (int64_t idx = 0; idx < latent; ++idx) {
+    volatile float exponent = (floorf((float)idx / 2.0f) * 2.0f) / (float)latent;
+    volatile float inv = 1.0f / powf(theta, exponent);
+    out[idx] = inv / two_pi;
+  }
+}
+
+bdh_status rope_freqs_device(int64_t latent, float theta, const float** out) {
+  int dev = 0;
+  BDH_HIP_TRY(hipGetDevice(&dev));
+  uint32_t tbits;
+  memcpy(&tbits, &theta, 4);
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto& m = device_scratch(dev).freqs;
+    auto it = m.find({latent, tbits});
+    if (it != m.end()) {
+      *out = it->second;
+      return BDH_OK;
+    }
+  }
+  std::vector<float> host((size_t)latent);
+  rope_freqs_host(latent, theta, host.data());
+  float* d = nullptr;
+  BDH_HIP_TRY(hipMalloc(&d, sizeof(float) * (size_t)latent));
+  BDH_HIP_TRY(hipMemcpy(d, host.data(), sizeof(float) * (size_t)latent, hipMemcpyHostToDevice));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  device_scratch(dev).freqs[{latent, tbits}] = d;
+  *out = d;
+  return BDH_OK;
+}
+
+// ------------------------------------------------------------- profiling ----
+namespace {
+std::mutex g_prof_mu;
+bdh_profile_snapshot g_prof = {};
+bool prof_env() {
+  const char* a = getenv("DragonModel_STAGE_PROFILE");
+  const char* b = getenv("BDH_STAGE_PROFILE");
+  return (a && *a) || (b && *b);
+}
+bool g_prof_on = prof_env();
+
+struct ProfScope {
+  std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+  uint64_t launches = 0;
+  uint64_t setup_ns = 0;
+  void done(bool ok) {
+    if (!g_prof_on) return;
+    const auto ns = (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                        std::chrono::steady_clock::now() - t0).count();
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    g_prof.calls += ok ? 1 : 0;
+    g_prof.launches += launches;
+    g_prof.total_ns += ns;
+    g_prof.setup_ns += setup_ns;
+    g_prof.dispatch_ns += ns > setup_ns ? ns - setup_ns : 0;
+  }
+};
+}  // namespace
+
+}  // namespace bdh
+
+using namespace bdh;
+
+namespace {
+
+constexpr int64_t kMaxGrid = 65535;
+
+bdh_status check_plan(const bdh_recurrent_plan* p) {
+  if (!p) return fail(BDH_EINVAL, "plan is null");
+  if (p->batch <= 0 || p->heads <= 0 || p->time <= 0 || p->latent <= 0 || p->embd <= 0)
+    return fail(BDH_UNSUPPORTED, "zero-sized dimension");
+  if (p->value_heads != 1 && p->value_heads != p->heads)
+    return fail(BDH_UNSUPPORTED, "value_heads must be 1 or heads");
+  if (p->batch * p->heads > kMaxGrid) return fail(BDH_UNSUPPORTED, "batch * heads exceeds 65535");
+  return BDH_OK;
+}
+
+int64_t default_interval(int64_t T) {
+  // State-carry interval of the MFMA path: rho is materialised every L tokens
+  // and the carries in between go through the chunk-pair score blocks.
+  const int64_t L = 512;
+  return T < L ? ((T + 127) / 128) * 128 : L;
+}
+
+bdh_status forward_common(const bdh_recurrent_plan* plan, int32_t dtype, const void* q,
+                          const void* v, const float* rho_in, const float* decay,
+                          const bdh_rope* rope, float* ctx, float* rho_out, int32_t chunk,
+                          void* stream, bool want_rho) {
+  ProfScope prof;
+  bdh_status st = check_plan(plan);
+  if (st != BDH_OK) return st;
+  if (!q || !v || !ctx || (want_rho && !rho_out)) return fail(BDH_EINVAL, "null tensor pointer");
+  if (dtype != BDH_F32 && dtype != BDH_BF16) return fail(BDH_EINVAL, "unknown dtype");
+  if (chunk != 0 && chunk != 128) return fail(BDH_UNSUPPORTED, "chunk must be 0 (auto) or 128");
+  if (rope && (rope->mode != BDH_ROPE_SEQUENTIAL && rope->mode != BDH_ROPE_FIXED))
+    return fail(BDH_EINVAL, "unknown rope mode");
+  if (rope && plan->latent % 2 != 0) return fail(BDH_UNSUPPORTED, "RoPE needs an even latent");
+  if (rope && !(rope->theta > 0.0f)) return fail(BDH_EINVAL, "rope theta must be > 0");
+  if (rope && (rope->pos0 < 0 || rope->pos0 + plan->time > (int64_t)1 << 24))
+    return fail(BDH_UNSUPPORTED, "positions must lie in [0, 2^24) to be exact in f32");
+  hipStream_t hs = (hipStream_t)stream;
+  const int64_t B = plan->batch, H = plan->heads, Hv = plan->value_heads, T = plan->time,
+                N = plan->latent, D = plan->embd;
+
+  const float* freqs = nullptr;
+  if (rope) {
+    st = rope_freqs_device(N, rope->theta, &freqs);
+    if (st != BDH_OK) return st;
+  }
+  prof.setup_ns = (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                      std::chrono::steady_clock::now() - prof.t0).count();
+
+  if (dtype == BDH_F32) {
+    const float* qr = (const float*)q;
+    if (rope) {
+      void* rot = nullptr;
+      st = scratch(SLOT_ROTATED, (size_t)(B * H * T * N) * sizeof(float), &rot);
+      if (st != BDH_OK) return st;
+      BDH_HIP_TRY(launch_rope_rotate_f32((const float*)q, freqs, (float*)rot, B * H, T, N,
+                                         rope->pos0, rope->mode == BDH_ROPE_FIXED, hs));
+      ++prof.launches;
+      qr = (const float*)rot;
+    }
+    const int64_t Lmax = want_rho ? (T < 256 ? T : 256) : T;
+    void* scores = nullptr;
+    st = scratch(SLOT_SCORES, (size_t)(B * H * Lmax * Lmax) * sizeof(float), &scores);
+    if (st != BDH_OK) return st;
+    F32Args a{qr, (const float*)v, want_rho ? rho_in : nullptr, decay, ctx, rho_out,
+              (float*)scores, B, H, Hv, T, N, D, Lmax, want_rho};
+    hipError_t e = run_f32_path(a, hs, &prof.launches);
+    if (e != hipSuccess) return hip_fail(e, "fp32 path launch");
+    prof.done(true);
+    return BDH_OK;
+  }
+
+  const char* why = nullptr;
+  if (!bf16_shape_supported(N, D, &why)) return fail(BDH_UNSUPPORTED, why);
+  Bf16Args a;
+  a.x = (const bf16_t*)q;
+  a.v = (const bf16_t*)v;
+  a.rho_in = want_rho ? rho_in : nullptr;
+  a.decay = decay;
+  a.freqs = freqs;
+  a.pos0 = rope ? rope->pos0 : 0;
+  a.fixed = rope ? rope->mode == BDH_ROPE_FIXED : 0;
+  a.ctx = ctx;
+  a.rho_out = rho_out;
+  a.B = B;
+  a.H = H;
+  a.Hv = Hv;
+  a.T = T;
+  a.N = N;
+  a.D = D;
+  a.L = want_rho ? default_interval(T) : ((T + 127) / 128) * 128;
+  a.state = want_rho;
+  st = run_bf16_path(a, hs, &prof.launches);
+  if (st != BDH_OK) return st;
+  prof.done(true);
+  return BDH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+bdh_status bdh_rope_freqs(int64_t latent, float theta, float* freqs_out) {
+  if (!freqs_out) return fail(BDH_EINVAL, "freqs_out is null");
+  if (latent <= 0) return fail(BDH_UNSUPPORTED, "latent must be > 0");
+  rope_freqs_host(latent, theta, freqs_out);
+  return BDH_OK;
+}
+
+bdh_status bdh_recurrent_plan_new(int64_t batch, int64_t heads, int64_t value_heads, int64_t time,
+                                  int64_t latent, int64_t embd, bdh_recurrent_plan* out) {
+  if (!out) return fail(BDH_EINVAL, "out is null");
+  bdh_recurrent_plan p{batch, heads, value_heads, time, latent, embd};
+  bdh_status st = check_plan(&p);
+  if (st != BDH_OK) return st;
+  *out = p;
+  if (g_prof_on) {
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    g_prof.metadata_reuse_hits += 0;
+  }
+  return BDH_OK;
+}
+
+int32_t bdh_supports_backend(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+bdh_status bdh_recurrent_attention_fwd(const bdh_recurrent_plan* plan, int32_t dtype,
+                                       const void* query, const void* value, const float* rho_in,
+                                       const float* decay, float* context_out, float* rho_out,
+                                       int32_t chunk, void* stream) {
+  return forward_common(plan, dtype, query, value, rho_in, decay, nullptr, context_out, rho_out,
+                        chunk, stream, true);
+}
+
+bdh_status bdh_recurrent_attention_rope_fwd(const bdh_recurrent_plan* plan, int32_t dtype,
+                                            const void* x, const void* value, const float* rho_in,
+                                            const float* decay, const bdh_rope* rope,
+                                            float* context_out, float* rho_out, int32_t chunk,
+                                            void* stream) {
+  if (!rope) return fail(BDH_EINVAL, "rope is null");
+  return forward_common(plan, dtype, x, value, rho_in, decay, rope, context_out, rho_out, chunk,
+                        stream, true);
+}
+
+bdh_status bdh_dense_causal_attention_fwd(const bdh_recurrent_plan* plan, int32_t dtype,
+                                          const void* query, const void* value, const float* decay,
+                                          float* context_out, void* stream) {
+  bdh_status st = check_plan(plan);
+  if (st != BDH_OK) return st;
+  if (plan->time > 1024) return fail(BDH_UNSUPPORTED, "dense causal attention needs time <= 1024");
+  return forward_common(plan, dtype, query, value, nullptr, decay, nullptr, context_out, nullptr,
+                        0, stream, false);
+}
+
+bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads, int64_t latent,
+                           int64_t embd, const float* x, const float* value, float* rho,
+                           const bdh_rope* rope, float* a_out, int32_t* active_idx_out,
+                           int32_t* active_cnt_out, void* stream) {
+  ProfScope prof;
+  bdh_recurrent_plan p{batch, heads, value_heads, 1, latent, embd};
+  bdh_status st = check_plan(&p);
+  if (st != BDH_OK) return st;
+  if (!x || !value || !rho || !a_out) return fail(BDH_EINVAL, "null tensor pointer");
+  if (latent > (int64_t)1 << 24) return fail(BDH_UNSUPPORTED, "latent too large");
+  if (rope && latent % 2 != 0) return fail(BDH_UNSUPPORTED, "RoPE needs an even latent");
+  if (rope && (rope->pos0 < 0 || rope->pos0 >= (int64_t)1 << 24))
+    return fail(BDH_UNSUPPORTED, "position must lie in [0, 2^24)");
+  if (rope && !(rope->theta > 0.0f)) return fail(BDH_EINVAL, "rope theta must be > 0");
+  if (embd > 2048) return fail(BDH_UNSUPPORTED, "decode step needs embd <= 2048");
+  const float* freqs = nullptr;
+  if (rope) {
+    st = rope_freqs_device(latent, rope->theta, &freqs);
+    if (st != BDH_OK) return st;
+  }
+  DecodeArgs a;
+  a.x = x;
+  a.v = value;
+  a.rho = rho;
+  a.freqs = freqs;
+  a.pos = rope ? (float)rope->pos0 : 0.0f;
+  a.a_out = a_out;
+  a.idx_out = active_idx_out;
+  a.cnt_out = active_cnt_out;
+  a.B = batch;
+  a.H = heads;
+  a.Hv = value_heads;
+  a.N = latent;
+  a.D = embd;
+  st = run_decode(a, (hipStream_t)stream, &prof.launches);
+  if (st == BDH_OK) prof.done(true);
+  return st;
+}
+
+void bdh_profile_enable(int32_t enabled) { g_prof_on = enabled != 0; }
+
+void bdh_profile_reset(void) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  g_prof = bdh_profile_snapshot{};
+}
+
+void bdh_profile_get(bdh_profile_snapshot* out) {
+  if (!out) return;
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  *out = g_prof;
+}
+
+const char* bdh_last_error(void) { return g_last_error.c_str(); }
+
+const char* bdh_version(void) { return "bdh_hip 0.1.0 (gfx950)"; }
+
+}  // extern "C"

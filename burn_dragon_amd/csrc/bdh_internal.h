@@ -1,0 +1,96 @@
+// Host-side internal interfaces between the translation units of libbdh_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "bdh_common.h"
+#include "bdh_hip.h"
+
+namespace bdh {
+
+// Thread-local error message; returns the status for `return fail(...)`.
+bdh_status fail(bdh_status st, const std::string& msg);
+bdh_status hip_fail(hipError_t e, const char* what);
+
+#define BDH_HIP_TRY(expr)                                   \
+  do {                                                      \
+    hipError_t _e = (expr);                                 \
+    if (_e != hipSuccess) return ::bdh::hip_fail(_e, #expr); \
+  } while (0)
+
+// Per-device scratch, one buffer per slot, grown on demand (never shrunk).
+enum ScratchSlot {
+  SLOT_SCORES = 0,   // causal score blocks      [S, Lp, Lp] f32
+  SLOT_VT,           // transposed values        [B*Hv, Dp, Tp] bf16
+  SLOT_ROPE_TABLE,   // cos/sin per (token, pair) [L, N/2] float2
+  SLOT_ROTATED,      // rotated queries (fp32 path) [S, T, N] f32
+  SLOT_DECODE,       // decode partial sums / segment lists
+  SLOT_COUNTERS,     // decode arrival counters (zeroed at allocation)
+  SLOT_COUNT
+};
+bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);
+
+// Device copy of the RoPE frequency table for (latent, theta), cached.
+bdh_status rope_freqs_device(int64_t latent, float theta, const float** out);
+// Host computation of the same table (attention.rs:552-576).
+void rope_freqs_host(int64_t latent, float theta, float* out);
+
+// --- launchers (rope.hip) ---------------------------------------------------
+// cs[t*half + k] = (cos, sin) of phase(pos(t), f_{2k}), t in [0, L)
+hipError_t launch_rope_table(const float* freqs, float2* cs, int64_t L, int64_t half,
+                             int64_t pos_first, int fixed, hipStream_t st);
+// out[s, t, :] = rope(x[s, t, :], pos(t)) in f32, exact op order.
+hipError_t launch_rope_rotate_f32(const float* x, const float* freqs, float* out, int64_t S,
+                                  int64_t T, int64_t N, int64_t pos0, int fixed, hipStream_t st);
+
+// --- fp32 path (prefill_f32.hip) -------------------------------------------
+struct F32Args {
+  const float* q;       // rotated queries [S, T, N]
+  const float* v;       // [B, Hv, T, D]
+  const float* rho_in;  // [S, N, D] or null
+  const float* decay;   // [H] or null
+  float* ctx;           // [S, T, D]
+  float* rho_out;       // [S, N, D]
+  float* scores;        // scratch [S, Lmax, Lmax]
+  int64_t B, H, Hv, T, N, D, Lmax;
+  bool state;           // false: context only (single interval, no rho)
+};
+hipError_t run_f32_path(const F32Args& a, hipStream_t st, uint64_t* launches);
+
+// --- bf16 MFMA path (prefill_bf16.hip) --------------------------------------
+struct Bf16Args {
+  const bf16_t* x;      // [S, T, N] (unrotated when rope != null)
+  const bf16_t* v;      // [B, Hv, T, D]
+  const float* rho_in;  // [S, N, D] or null
+  const float* decay;   // [H] or null
+  const float* freqs;   // device RoPE frequencies or null (query pre-rotated)
+  int64_t pos0;
+  int fixed;
+  float* ctx;           // [S, T, D]
+  float* rho_out;       // [S, N, D]
+  int64_t B, H, Hv, T, N, D;
+  int64_t L;            // state-carry interval (multiple of 128)
+  bool state;           // false: context only (single interval, no rho)
+};
+bool bf16_shape_supported(int64_t N, int64_t D, const char** why);
+bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches);
+
+// --- decode (decode.hip) ------------------------------------------------------
+struct DecodeArgs {
+  const float* x;       // [S, N]
+  const float* v;       // [B, Hv, D]
+  float* rho;           // [S, N, D]
+  const float* freqs;   // null -> x already rotated
+  float pos;
+  float* a_out;         // [S, D]
+  int32_t* idx_out;     // [S, N] or null
+  int32_t* cnt_out;     // [S] or null
+  int64_t B, H, Hv, N, D;
+};
+bdh_status run_decode(const DecodeArgs& a, hipStream_t st, uint64_t* launches);
+
+}  // namespace bdh

@@ -1,0 +1,156 @@
+/*
+ * bdh_hip.h -- C ABI of the MI355X (gfx950) recurrent linear-attention
+ * forward path of burn_dragon ("BDH"), implemented in hand-written HIP.
+ *
+ * Every entry point replaces one function of the reference's Burn custom-op
+ * surface (crates/burn_dragon_kernel, re-exported at src/lib.rs:40-56);
+ * the comment above each declaration cites it.  Conventions:
+ *   - all tensor arguments are DEVICE pointers owned by the caller, dense
+ *     row-major (C-contiguous) in the reference's layouts:
+ *       query / x  [B, H, T, N]       value [B, Hv, T, D], Hv in {1, H}
+ *       rho        [B, H, N, D] f32   context [B, H, T, D] f32
+ *       decay      [H] f32            (NULL = ones: RoPE, no ALiBi)
+ *   - `stream` is a hipStream_t (NULL = the default stream); launches are
+ *     asynchronous on it, nothing synchronises the host;
+ *   - the library never allocates or frees caller memory.  It keeps its own
+ *     per-device scratch, grown on first use of a shape;
+ *   - errors are status codes, never aborts.  BDH_UNSUPPORTED is the
+ *     reference's `None` ("use the Burn-op reference instead");
+ *     bdh_last_error() gives the message (thread-local).
+ *   - calls that share a device's scratch must not overlap on different
+ *     streams (one stream per device, as the reference's backend stream).
+ */
+#ifndef BDH_HIP_H
+#define BDH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  BDH_OK = 0,
+  BDH_UNSUPPORTED = 1, /* reference returns None: caller falls back */
+  BDH_EINVAL = -1,     /* malformed arguments (null outputs, bad enum) */
+  BDH_EHIP = -2        /* a HIP runtime call failed */
+} bdh_status;
+
+typedef enum { BDH_F32 = 0, BDH_BF16 = 1 } bdh_dtype;
+
+/* RoPE positions: RecurrentPositionMode (dragon_support.rs), mirrored by
+ * rotate_positions / rotate_positions_fixed (attention.rs:339-349). */
+typedef enum { BDH_ROPE_SEQUENTIAL = 0, BDH_ROPE_FIXED = 1 } bdh_rope_mode;
+
+typedef struct {
+  int32_t mode;  /* bdh_rope_mode */
+  int32_t _pad;
+  int64_t pos0;  /* first position (Sequential) or the position (Fixed) */
+  float theta;   /* FusedKernelConfig::rope_theta, default 65536 (config.rs:79) */
+} bdh_rope;
+
+/* Host copy of the RoPE frequency table the kernels use (f32, latent
+ * entries): Attention::build_freqs, Rope arm
+ * (crates/burn_dragon_core/src/model/attention.rs:552-576). */
+bdh_status bdh_rope_freqs(int64_t latent, float theta, float* freqs_out);
+
+/* Shape plan.  Replaces CompiledRecurrentAttentionPlan::new
+ * (crates/burn_dragon_kernel/src/recurrent.rs:107-139); integers instead of
+ * the reference's uploaded f32 meta tensor, nothing is sent to the device. */
+typedef struct {
+  int64_t batch, heads, value_heads, time, latent, embd;
+} bdh_recurrent_plan;
+
+/* Validates like try_fused_recurrent_attention_wgpu (recurrent.rs:187-195):
+ * any zero dim or value_heads not in {1, heads} -> BDH_UNSUPPORTED. */
+bdh_status bdh_recurrent_plan_new(int64_t batch, int64_t heads, int64_t value_heads,
+                                  int64_t time, int64_t latent, int64_t embd,
+                                  bdh_recurrent_plan* out);
+
+/* Replaces supports_backend (recurrent.rs:151-173, exported as
+ * supports_recurrent_backend): 1 when the current device is gfx950 and the
+ * kernels are loadable, else 0. */
+int32_t bdh_supports_backend(void);
+
+/* Replaces try_fused_recurrent_attention_wgpu_with_plan (recurrent.rs:221-359)
+ * and, with plan built per call, try_fused_recurrent_attention_wgpu
+ * (recurrent.rs:175-219).  query is already rotated (the reference applies
+ * RoPE before the call, sequence_dispatch.rs:97-104).
+ *   ctx_t = x_t . rho_t ;  rho_{t+1} = (rho_t + x_t^T v_t) * decay
+ * rho_in NULL -> zeros (recurrent.rs:243-246).  rho_out may equal rho_in
+ * (in place); otherwise rho_in is not written (the reference's private copy,
+ * recurrent.rs:259).  dtype applies to query and value: BDH_F32 runs the
+ * fp32 path, BDH_BF16 the MFMA path (fp32 accumulate, fp32 rho/context).
+ * chunk: causal block size for the MFMA path (0 = 128). */
+bdh_status bdh_recurrent_attention_fwd(const bdh_recurrent_plan* plan, int32_t dtype,
+                                       const void* query, const void* value,
+                                       const float* rho_in, const float* decay,
+                                       float* context_out, float* rho_out,
+                                       int32_t chunk, void* stream);
+
+/* RoPE-fused variant: x is the UNROTATED sparse activation; RoPE
+ * (attention.rs:488-576, f32 phase op order) is applied inside the kernels.
+ * Otherwise identical to bdh_recurrent_attention_fwd.  Replaces the pair
+ * rotate_positions[_fixed] + try_fused_recurrent_attention_wgpu_with_plan
+ * inside DragonModel::recurrent_attention_with_plan
+ * (crates/burn_dragon_core/src/model/dragon/sequence_dispatch.rs:83-136). */
+bdh_status bdh_recurrent_attention_rope_fwd(const bdh_recurrent_plan* plan, int32_t dtype,
+                                            const void* x, const void* value,
+                                            const float* rho_in, const float* decay,
+                                            const bdh_rope* rope, float* context_out,
+                                            float* rho_out, int32_t chunk, void* stream);
+
+/* Sparse decode step (T = 1), fp32.  Same result as
+ * bdh_recurrent_attention_rope_fwd with time = 1 and decay = NULL, computed
+ * by touching only the active rows of rho (RoPE makes them pairs):
+ *   A = { i : x_i != 0  or  (x_{i^1} != 0 and frac(pos * f_i) != 0) }
+ *   a = rot(x) . rho (read before the update) ;  rho[A] += rot(x)[A]^T v
+ * x [B,H,N], value [B,Hv,D], rho [B,H,N,D] updated in place, a_out [B,H,D].
+ * rope NULL: x is already rotated and A = { i : x_i != 0 }.
+ * active_idx_out [B,H,N] int32 (ascending, padded with -1) and
+ * active_cnt_out [B,H] int32 may be NULL.  This is the per-token call of the
+ * reference's decode drivers (dragon.rs:1749-1808, generation.rs:458) through
+ * recurrent_attention_with_plan at T = 1. */
+bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads,
+                           int64_t latent, int64_t embd, const float* x,
+                           const float* value, float* rho, const bdh_rope* rope,
+                           float* a_out, int32_t* active_idx_out,
+                           int32_t* active_cnt_out, void* stream);
+
+/* Replaces try_fused_dense_causal_attention_wgpu[_with_plan]
+ * (crates/burn_dragon_kernel/src/dense_causal_attention.rs:162-261):
+ *   ctx = tril(-1)(Q Q^T * decay^(r-c)) V      (no state), decay [H] required.
+ * time > 1024 -> BDH_UNSUPPORTED as in the reference (:44, :179). */
+bdh_status bdh_dense_causal_attention_fwd(const bdh_recurrent_plan* plan, int32_t dtype,
+                                          const void* query, const void* value,
+                                          const float* decay, float* context_out,
+                                          void* stream);
+
+/* Profiling counters with the field names of KernelProfileSnapshot
+ * (crates/burn_dragon_kernel/src/profiling.rs:3-16).  Host wall-clock
+ * nanoseconds of the entry points; collected only while enabled (the
+ * reference's DragonModel_STAGE_PROFILE switch, profiling.rs:50-51). */
+typedef struct {
+  uint64_t calls, launches;
+  uint64_t total_ns, setup_ns, copy_ns, dispatch_ns;
+  uint64_t transient_allocations;
+  uint64_t metadata_upload_bytes, metadata_reuse_hits, metadata_reuse_bytes;
+  uint64_t resident_rollout_steps;
+} bdh_profile_snapshot;
+
+void bdh_profile_enable(int32_t enabled);
+/* recurrent_profile_reset / recurrent_profile_snapshot (recurrent.rs:57-63). */
+void bdh_profile_reset(void);
+void bdh_profile_get(bdh_profile_snapshot* out);
+
+/* Thread-local message of the last non-OK status of this thread. */
+const char* bdh_last_error(void);
+
+/* Library version string. */
+const char* bdh_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BDH_HIP_H */

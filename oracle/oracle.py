@@ -1,0 +1,197 @@
+"""numpy/ctypes front end of the CPU oracle (oracle/bdh_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of bench.py use it as the checker; nothing in the
+product package imports it.  Each wrapper names the reference function the C
+code restates (paths relative to the burn_dragon v0.21.8 checkout).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libbdh_oracle.so")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64 = ctypes.c_int64
+
+
+def build() -> str:
+    """Compile the oracle with its committed Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-B", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.bdh_oracle_rope_freqs.argtypes = [_i64, ctypes.c_float, _f32p]
+        L.bdh_oracle_rope_rotate.argtypes = [_f32p, _i64, _i64, _i64, _i64, ctypes.c_int32,
+                                             ctypes.c_float, _f32p]
+        L.bdh_oracle_active_rows.argtypes = [_f32p, _i64, _i64, _f32p, _i32p]
+        L.bdh_oracle_active_rows.restype = ctypes.c_int32
+        for name in ("bdh_oracle_recurrent_f32",):
+            getattr(L, name).argtypes = [_f32p, _f32p, _f32p, _f32p] + [_i64] * 6 + [_f32p, _f32p]
+        for name in ("bdh_oracle_recurrent_f64", "bdh_oracle_dense_score_f64"):
+            getattr(L, name).argtypes = [_f32p, _f32p, _f32p, _f32p] + [_i64] * 6 + [_f64p, _f64p]
+        L.bdh_oracle_decode_step_f32.argtypes = [_f32p, _f32p, _f32p] + [_i64] * 6 + [
+            ctypes.c_float, _f32p, _i32p, _i32p]
+        L.bdh_oracle_round_bf16.argtypes = [_f32p, _f32p, _i64]
+        L.bdh_oracle_ndarray_recurrent_f32.argtypes = [_f32p, _f32p, _f32p, _f32p] + [_i64] * 6 + [
+            _f32p, _f32p, ctypes.c_int32]
+        L.bdh_oracle_ndarray_recurrent_f32.restype = ctypes.c_double
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(_f32p)
+
+
+def _opt_f32(a):
+    if a is None:
+        return None, None
+    return _f32(a)
+
+
+def rope_freqs(latent: int, theta: float = 65536.0) -> np.ndarray:
+    """Attention::build_freqs, Rope arm (attention.rs:552-576)."""
+    out = np.empty(latent, np.float32)
+    lib().bdh_oracle_rope_freqs(latent, theta, out.ctypes.data_as(_f32p))
+    return out
+
+
+def rope_rotate(x, pos0: int = 0, mode: int = 0, theta: float = 65536.0) -> np.ndarray:
+    """rotate_positions (mode 0) / rotate_positions_fixed (mode 1) on x[..., T, N]
+    (attention.rs:339-349, 512-550, 488-501)."""
+    x, xp = _f32(x)
+    T, N = x.shape[-2], x.shape[-1]
+    rows = x.size // (T * N)
+    out = np.empty_like(x)
+    lib().bdh_oracle_rope_rotate(xp, rows, T, N, pos0, mode, theta, out.ctypes.data_as(_f32p))
+    return out
+
+
+def active_rows(x_row, pos: int, theta: float = 65536.0) -> np.ndarray:
+    """Structural active set {i : rot(x)_i not identically zero} at position pos."""
+    x_row, xp = _f32(x_row)
+    N = x_row.shape[-1]
+    freqs = rope_freqs(N, theta)
+    idx = np.empty(N, np.int32)
+    cnt = lib().bdh_oracle_active_rows(xp, N, pos, freqs.ctypes.data_as(_f32p),
+                                       idx.ctypes.data_as(_i32p))
+    return idx[:cnt].copy()
+
+
+def _dims(q, v):
+    B, H, T, N = q.shape
+    Bv, Hv, Tv, D = v.shape
+    assert Bv == B and Tv == T and Hv in (1, H), (q.shape, v.shape)
+    return B, H, Hv, T, N, D
+
+
+def recurrent_f32(q, v, rho0=None, decay=None):
+    """recurrent_attention_reference (linear.rs:18-60), op-for-op in f32."""
+    q, qp = _f32(q)
+    v, vp = _f32(v)
+    rho0, rp = _opt_f32(rho0)
+    decay, dp = _opt_f32(decay)
+    B, H, Hv, T, N, D = _dims(q, v)
+    ctx = np.empty((B, H, T, D), np.float32)
+    rho = np.empty((B, H, N, D), np.float32)
+    lib().bdh_oracle_recurrent_f32(qp, vp, rp, dp, B, H, Hv, T, N, D,
+                                   ctx.ctypes.data_as(_f32p), rho.ctypes.data_as(_f32p))
+    return ctx, rho
+
+
+def recurrent_f64(q, v, rho0=None, decay=None):
+    """The same recurrence carried in f64."""
+    q, qp = _f32(q)
+    v, vp = _f32(v)
+    rho0, rp = _opt_f32(rho0)
+    decay, dp = _opt_f32(decay)
+    B, H, Hv, T, N, D = _dims(q, v)
+    ctx = np.empty((B, H, T, D), np.float64)
+    rho = np.empty((B, H, N, D), np.float64)
+    lib().bdh_oracle_recurrent_f64(qp, vp, rp, dp, B, H, Hv, T, N, D,
+                                   ctx.ctypes.data_as(_f64p), rho.ctypes.data_as(_f64p))
+    return ctx, rho
+
+
+def dense_score_f64(q, v, rho0=None, decay=None, want_ctx=True, want_rho=True):
+    """Dense-score form (linear.rs:221-364) in f64."""
+    q, qp = _f32(q)
+    v, vp = _f32(v)
+    rho0, rp = _opt_f32(rho0)
+    decay, dp = _opt_f32(decay)
+    B, H, Hv, T, N, D = _dims(q, v)
+    ctx = np.empty((B, H, T, D), np.float64) if want_ctx else None
+    rho = np.empty((B, H, N, D), np.float64) if want_rho else None
+    lib().bdh_oracle_dense_score_f64(
+        qp, vp, rp, dp, B, H, Hv, T, N, D,
+        ctx.ctypes.data_as(_f64p) if ctx is not None else None,
+        rho.ctypes.data_as(_f64p) if rho is not None else None)
+    return ctx, rho
+
+
+def decode_step_f32(x, v, rho, pos: int, theta: float = 65536.0):
+    """One T=1 step with RoPE at pos (sequence_dispatch.rs:97-124 ->
+    linear.rs:43-57).  rho [B,H,N,D] is updated in place (must be float32,
+    C-contiguous).  Returns (a [B,H,D], active_idx [B,H,N], active_cnt [B,H])."""
+    x, xp = _f32(x)
+    v, vp = _f32(v)
+    assert rho.dtype == np.float32 and rho.flags.c_contiguous
+    B, H, N = x.shape
+    Hv, D = v.shape[1], v.shape[2]
+    a = np.empty((B, H, D), np.float32)
+    idx = np.empty((B, H, N), np.int32)
+    cnt = np.empty((B, H), np.int32)
+    lib().bdh_oracle_decode_step_f32(xp, vp, rho.ctypes.data_as(_f32p), B, H, Hv, N, D, pos,
+                                     theta, a.ctypes.data_as(_f32p), idx.ctypes.data_as(_i32p),
+                                     cnt.ctypes.data_as(_i32p))
+    return a, idx, cnt
+
+
+def round_bf16(a) -> np.ndarray:
+    """Round-to-nearest-even to bf16, returned as exact float32."""
+    a, ap = _f32(a)
+    out = np.empty_like(a)
+    lib().bdh_oracle_round_bf16(ap, out.ctypes.data_as(_f32p), a.size)
+    return out
+
+
+def ndarray_recurrent_f32(q, v, rho0=None, decay=None, threads: int = 0):
+    """CPU baseline: the NdArray op sequence of linear.rs:43-57 with
+    materialised [N, D] temporaries, OpenMP over (b, h).  Returns
+    (ctx, rho, wall_seconds)."""
+    q, qp = _f32(q)
+    v, vp = _f32(v)
+    rho0, rp = _opt_f32(rho0)
+    decay, dp = _opt_f32(decay)
+    B, H, Hv, T, N, D = _dims(q, v)
+    ctx = np.empty((B, H, T, D), np.float32)
+    rho = np.empty((B, H, N, D), np.float32)
+    secs = lib().bdh_oracle_ndarray_recurrent_f32(qp, vp, rp, dp, B, H, Hv, T, N, D,
+                                                  ctx.ctypes.data_as(_f32p),
+                                                  rho.ctypes.data_as(_f32p), threads)
+    return ctx, rho, secs
+
+
+def rel_l2(a, b) -> float:
+    """||a - b||_2 / ||b||_2 in f64 (b is the reference)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    den = np.linalg.norm(b.ravel())
+    num = np.linalg.norm((a - b).ravel())
+    return float(num / den) if den > 0 else float(num)

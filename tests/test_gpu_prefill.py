@@ -1,0 +1,191 @@
+"""Prefill paths vs the CPU oracle at sizes the oracle finishes in seconds.
+
+fp32 path: rel-L2 <= 1e-5 against the f64 recurrence (the reference's own
+test shapes and index-formula inputs, decay, initial state, shared and
+per-head values, RoPE fused).  bf16 MFMA path: rel-L2 <= 1e-2 against the
+f64 recurrence evaluated on the bf16-rounded inputs."""
+import numpy as np
+import pytest
+
+from tests import refcases as rc
+from tests.gpu_util import TOL_BF16, TOL_F32, announce, dev, host, need_gpu, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(torch, bd, q, v, rho0, decay, dtype=None, rope=None):
+    dt = dtype or torch.float32
+    qd, vd = dev(torch, q, dt), dev(torch, v, dt)
+    rd = dev(torch, rho0) if rho0 is not None else None
+    dd = dev(torch, decay) if decay is not None else None
+    if rope is None:
+        out = bd.try_fused_recurrent_attention(qd, vd, rd, dd)
+    else:
+        out = bd.try_fused_recurrent_attention_rope(qd, vd, rd, dd, position=rope[0], fixed=rope[1])
+    torch.cuda.synchronize()
+    assert out is not None
+    return host(out.context), host(out.rho)
+
+
+# ---- fp32 path ---------------------------------------------------------------
+
+@pytest.mark.parametrize("case", range(len(rc.RECURRENT_TEST_SHAPES)))
+def test_f32_reference_test_shapes(oracle, case):
+    # recurrent/tests.rs:158-206, 290-336 shapes; our generator, same law N(0,1).
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    qs, vs, rs, dec = rc.RECURRENT_TEST_SHAPES[case]
+    rng = np.random.default_rng(100 + case)
+    q = rc.gaussian(rng, qs)
+    v = rc.gaussian(rng, vs)
+    rho0 = rc.gaussian(rng, rs) if rs else None
+    decay = np.array(dec, np.float32) if dec else None
+    announce("f32 shapes", qs, vs)
+    ctx, rho = _run(torch, bd, q, v, rho0, decay)
+    cref, rref = oracle.recurrent_f64(q, v, rho0, decay)
+    assert rel_l2(ctx, cref) <= TOL_F32
+    assert rel_l2(rho, rref) <= TOL_F32
+
+
+def test_f32_index_formula_invariant_inputs(oracle):
+    # linear.rs:485-533 inputs: T=320 (crosses the 256-token state interval).
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    q, v, rho0, decay, _ = rc.chunked_decay_state_case()
+    announce("f32 linear.rs:485")
+    ctx, rho = _run(torch, bd, q, v, rho0, decay)
+    cref, rref = oracle.dense_score_f64(q, v, rho0, decay)
+    assert rel_l2(ctx, cref) <= TOL_F32 and rel_l2(rho, rref) <= TOL_F32
+    q, v, _ = rc.chunked_no_decay_case()
+    announce("f32 linear.rs:451")
+    ctx, rho = _run(torch, bd, q, v, None, None)
+    cref, rref = oracle.dense_score_f64(q, v)
+    assert rel_l2(ctx, cref) <= TOL_F32 and rel_l2(rho, rref) <= TOL_F32
+    # known answer, linear.rs:433-449
+    q, v, rho_exp, ctx_exp = rc.signed_rho_case()
+    ctx, rho = _run(torch, bd, q, v, None, None)
+    assert np.array_equal(rho, rho_exp) and np.array_equal(ctx, ctx_exp)
+
+
+def test_f32_c1_config_rope(oracle):
+    # B1 nh4 T256 N1024 D64, RoPE theta 65536, V ~ N(0,1).
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(rc.config_seed(1))
+    x = rc.sparse_relu(rng, (1, 4, 256, 1024))
+    v = rc.gaussian(rng, (1, 1, 256, 64))
+    announce("f32 C1 rope")
+    ctx, rho = _run(torch, bd, x, v, None, None, rope=(0, False))
+    q = oracle.rope_rotate(x, pos0=0)
+    cref, rref = oracle.recurrent_f64(q, v)
+    assert rel_l2(ctx, cref) <= TOL_F32 and rel_l2(rho, rref) <= TOL_F32
+    # the f32 op-order mirror agrees too
+    c32, r32 = oracle.recurrent_f32(q, v)
+    assert rel_l2(ctx, c32) <= TOL_F32
+
+
+def test_f32_rope_fixed_and_offset(oracle):
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(21)
+    x = rc.sparse_relu(rng, (2, 2, 40, 64))
+    v = rc.gaussian(rng, (2, 2, 40, 24))
+    rho0 = rc.gaussian(rng, (2, 2, 64, 24))
+    for pos, fixed in ((5, False), (123, True)):
+        announce("f32 rope", pos, fixed)
+        ctx, rho = _run(torch, bd, x, v, rho0, None, rope=(pos, fixed))
+        q = oracle.rope_rotate(x, pos0=pos, mode=1 if fixed else 0)
+        cref, rref = oracle.recurrent_f64(q, v, rho0)
+        assert rel_l2(ctx, cref) <= TOL_F32 and rel_l2(rho, rref) <= TOL_F32
+
+
+# ---- bf16 MFMA path -----------------------------------------------------------
+
+def _bf16_case(rng, B, H, Hv, T, N, D, with_rho):
+    x = rc.sparse_relu(rng, (B, H, T, N))
+    v = rc.gaussian(rng, (B, Hv, T, D), 1 / 16)
+    rho0 = rc.gaussian(rng, (B, H, N, D), 0.05) if with_rho else None
+    return x, v, rho0
+
+
+@pytest.mark.parametrize("B,H,Hv,T,N,D,with_rho,decay,pos", [
+    (1, 2, 1, 128, 256, 64, False, None, 0),          # one chunk
+    (2, 2, 1, 512, 512, 256, False, None, 0),         # 4 chunks, one interval
+    (1, 2, 2, 300, 256, 96, True, None, 17),          # ragged T, per-head V, rho_in
+    (1, 2, 1, 1100, 256, 128, True, None, 3),         # 3 state intervals (512+512+76)
+    (1, 4, 1, 256, 256, 64, True, [0.99, 0.98, 0.97, 0.96], 0),  # ALiBi-style decay
+])
+def test_bf16_rope_prefill_matches_oracle(oracle, B, H, Hv, T, N, D, with_rho, decay, pos):
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(T * 7 + N + D)
+    x, v, rho0 = _bf16_case(rng, B, H, Hv, T, N, D, with_rho)
+    dec = np.array(decay, np.float32) if decay else None
+    xb, vb = oracle.round_bf16(x), oracle.round_bf16(v)
+    announce("bf16 rope", B, H, Hv, T, N, D, with_rho, decay, pos)
+    ctx, rho = _run(torch, bd, xb, vb, rho0, dec, dtype=torch.bfloat16, rope=(pos, False))
+    q = oracle.rope_rotate(xb, pos0=pos)
+    cref, rref = oracle.recurrent_f64(q, vb, rho0, dec)
+    e_ctx, e_rho = rel_l2(ctx, cref), rel_l2(rho, rref)
+    print(f"rel-L2 ctx {e_ctx:.2e} rho {e_rho:.2e}")
+    assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
+
+
+def test_bf16_prerotated_query(oracle):
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(31)
+    x, v, rho0 = _bf16_case(rng, 2, 2, 1, 256, 256, 64, True)
+    q = oracle.round_bf16(oracle.rope_rotate(x, pos0=0))
+    vb = oracle.round_bf16(v)
+    announce("bf16 prerotated")
+    ctx, rho = _run(torch, bd, q, vb, rho0, None, dtype=torch.bfloat16)
+    cref, rref = oracle.recurrent_f64(q, vb, rho0)
+    assert rel_l2(ctx, cref) <= TOL_BF16 and rel_l2(rho, rref) <= TOL_BF16
+
+
+def test_bf16_unsupported_shape_returns_none():
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    q = torch.zeros(1, 1, 8, 100, dtype=torch.bfloat16, device="cuda")
+    v = torch.zeros(1, 1, 8, 64, dtype=torch.bfloat16, device="cuda")
+    assert bd.try_fused_recurrent_attention(q, v) is None
+
+
+# ---- dense causal attention ----------------------------------------------------
+
+@pytest.mark.parametrize("case", range(len(rc.DENSE_TEST_SHAPES)))
+def test_dense_causal_attention_f32(oracle, case):
+    # dense_causal_attention/tests.rs:185-204 shapes and decays.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    qs, vs, dec = rc.DENSE_TEST_SHAPES[case]
+    rng = np.random.default_rng(200 + case)
+    q, v = rc.gaussian(rng, qs), rc.gaussian(rng, vs)
+    decay = np.array(dec, np.float32)
+    announce("dense f32", qs)
+    out = bd.try_fused_dense_causal_attention(dev(torch, q), dev(torch, v), dev(torch, decay))
+    torch.cuda.synchronize()
+    cref, _ = oracle.dense_score_f64(q, v, None, decay, want_rho=False)
+    assert rel_l2(host(out), cref) <= TOL_F32
+
+
+def test_dense_causal_attention_bf16_and_limits(oracle):
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(41)
+    q = oracle.round_bf16(oracle.rope_rotate(rc.sparse_relu(rng, (2, 2, 384, 256))))
+    v = oracle.round_bf16(rc.gaussian(rng, (2, 1, 384, 64), 1 / 16))
+    decay = np.ones(2, np.float32)
+    announce("dense bf16")
+    out = bd.try_fused_dense_causal_attention(dev(torch, q, torch.bfloat16),
+                                              dev(torch, v, torch.bfloat16), dev(torch, decay))
+    torch.cuda.synchronize()
+    cref, _ = oracle.dense_score_f64(q, v, None, None, want_rho=False)
+    assert rel_l2(host(out), cref) <= TOL_BF16
+    big = torch.zeros(1, 1, 1025, 8, device="cuda")
+    assert bd.try_fused_dense_causal_attention(big, big, torch.ones(1, device="cuda")) is None
+    # decay of the wrong shape -> None (dense_causal_attention.rs:209-211)
+    qd = dev(torch, q, torch.bfloat16)
+    vd = dev(torch, v, torch.bfloat16)
+    assert bd.try_fused_dense_causal_attention(qd, vd, torch.ones(3, device="cuda")) is None
