@@ -24,12 +24,10 @@ bdh_status hip_fail(hipError_t e, const char* what);
 
 // Per-device scratch, one buffer per slot, grown on demand (never shrunk).
 enum ScratchSlot {
-  SLOT_SCORES = 0,   // causal score blocks      [S, Lp, Lp] f32
+  SLOT_SCORES = 0,   // causal score partials    [KS, S, n_iv, Lp, Lp] f32
   SLOT_VT,           // transposed values        [B*Hv, Dp, Tp] bf16
-  SLOT_ROPE_TABLE,   // cos/sin per (token, pair) [L, N/2] float2
+  SLOT_ROPE_TABLE,   // packed bf16 cos/sin per (token, pair) [T, N/2]
   SLOT_ROTATED,      // rotated queries (fp32 path) [S, T, N] f32
-  SLOT_DECODE,       // decode partial sums / segment lists
-  SLOT_COUNTERS,     // decode arrival counters (zeroed at allocation)
   SLOT_COUNT
 };
 bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);
@@ -40,9 +38,6 @@ bdh_status rope_freqs_device(int64_t latent, float theta, const float** out);
 void rope_freqs_host(int64_t latent, float theta, float* out);
 
 // --- launchers (rope.hip) ---------------------------------------------------
-// cs[t*half + k] = (cos, sin) of phase(pos(t), f_{2k}), t in [0, L)
-hipError_t launch_rope_table(const float* freqs, float2* cs, int64_t L, int64_t half,
-                             int64_t pos_first, int fixed, hipStream_t st);
 // out[s, t, :] = rope(x[s, t, :], pos(t)) in f32, exact op order.
 hipError_t launch_rope_rotate_f32(const float* x, const float* freqs, float* out, int64_t S,
                                   int64_t T, int64_t N, int64_t pos0, int fixed, hipStream_t st);

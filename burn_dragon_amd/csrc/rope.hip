@@ -1,34 +1,9 @@
-// RoPE on gfx950: per-(token, pair) cos/sin tables for the MFMA path and an
-// exact-op-order rotation for the fp32 path.  Both compute the phase as the
-// reference does (attention.rs:540-550): raw = p * f, (raw - floor(raw)) * 2pi
-// in f32, then cos/sin.
+// RoPE rotation for the fp32 path, in the reference's exact f32 op order
+// (attention.rs:540-550): raw = p * f, (raw - floor(raw)) * 2pi, cos/sin,
+// then x*cos + rotated*sin.
 #include "bdh_internal.h"
 
 namespace bdh {
-
-__global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict__ freqs,
-                                                         float2* __restrict__ cs, int64_t L,
-                                                         int64_t half, int64_t pos_first,
-                                                         int fixed) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= L * half) return;
-  const int64_t t = i / half;
-  const int64_t k = i - t * half;
-  const float p = (float)(fixed ? pos_first : pos_first + t);
-  const float ph = rope_phase(p, freqs[2 * k]);
-  float s, c;
-  sincosf(ph, &s, &c);
-  cs[i] = make_float2(c, s);
-}
-
-hipError_t launch_rope_table(const float* freqs, float2* cs, int64_t L, int64_t half,
-                             int64_t pos_first, int fixed, hipStream_t st) {
-  const int64_t n = L * half;
-  if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                     freqs, cs, L, half, pos_first, fixed);
-  return hipGetLastError();
-}
 
 // One thread per (row, pair): out = [even*c - odd*s, odd*c + even*s], each op
 // rounded separately like the reference's element-wise tensor ops.
