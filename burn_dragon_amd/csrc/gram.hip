@@ -33,44 +33,40 @@ __device__ __forceinline__ void gram_tile(const TileCtx& t, int kb, int ke, bf16
   const bool active = (!DIAG || wn * 128 < wm * 64 + 64) && t.ri + wm * 64 < t.Lc &&
                       t.rj + wn * 128 < t.Lc;
 
-  uint4 ra[VPT], rb[VPT], ca[VPT], cb[VPT];
+  struct Stage {
+    uint4 ra[VPT], rb[VPT], ca[VPT], cb[VPT];
+  };
   const int kv = tid & 3;
-  auto load = [&](int kt) {
+  auto load = [&](Stage& S, int kt) {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int row = (tid + i * NT) >> 2;
       const int64_t k = (int64_t)kt * BK + kv * 8;
-      // rows past the interval: load a valid row, then zero the values
+      // Rows past the interval re-read the last valid row: the scores of
+      // such rows and columns are never written, so no masking is needed
+      // (and none may be: a select here would wait for the load).
       const int64_t ti = t.ri + row;
       const int64_t tic = ti < t.Lc ? ti : t.Lc - 1;
-      const uint4 xa = ldg16(t.X + tic * t.N + k);
-      ra[i] = ti < t.Lc ? xa : make_uint4(0, 0, 0, 0);
-      if (ROPE) ca[i] = ldg16(t.CS + tic * t.half + k / 2);
+      S.ra[i] = ldg16(t.X + tic * t.N + k);
+      if (ROPE) S.ca[i] = ldg16(t.CS + tic * t.half + k / 2);
       if (!DIAG) {
         const int64_t tj = t.rj + row;
         const int64_t tjc = tj < t.Lc ? tj : t.Lc - 1;
-        const uint4 xb = ldg16(t.X + tjc * t.N + k);
-        rb[i] = tj < t.Lc ? xb : make_uint4(0, 0, 0, 0);
-        if (ROPE) cb[i] = ldg16(t.CS + tjc * t.half + k / 2);
+        S.rb[i] = ldg16(t.X + tjc * t.N + k);
+        if (ROPE) S.cb[i] = ldg16(t.CS + tjc * t.half + k / 2);
       }
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](const Stage& S, int buf) {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int row = (tid + i * NT) >> 2;
-      *reinterpret_cast<uint4*>(&As[buf][row * LDP + kv * 8]) = prep8<ROPE>(ra[i], ca[i], 1.0f, false);
+      *reinterpret_cast<uint4*>(&As[buf][row * LDP + kv * 8]) = prep8<ROPE>(S.ra[i], S.ca[i], 1.0f, false);
       if (!DIAG)
-        *reinterpret_cast<uint4*>(&Bs[buf][row * LDP + kv * 8]) = prep8<ROPE>(rb[i], cb[i], 1.0f, false);
+        *reinterpret_cast<uint4*>(&Bs[buf][row * LDP + kv * 8]) = prep8<ROPE>(S.rb[i], S.cb[i], 1.0f, false);
     }
   };
-
-  load(kb);
-  store(0);
-  __syncthreads();
-  for (int kt = kb; kt < ke; ++kt) {
-    const int buf = (kt - kb) & 1;
-    if (kt + 1 < ke) load(kt + 1);
+  auto compute = [&](int buf) {
     if (active) {
       const bf16_t* Ab = As[buf];
       const bf16_t* Bb = DIAG ? As[buf] : Bs[buf];
@@ -90,7 +86,24 @@ __device__ __forceinline__ void gram_tile(const TileCtx& t, int kb, int ke, bf16
           for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32(af[mi], bfr[ni], acc[mi][ni]);
       }
     }
-    if (kt + 1 < ke) store(buf ^ 1);
+  };
+
+  // Pipeline: LDS holds step kt (buffer (kt - kb) & 1); the register ring
+  // holds steps kt+1 and kt+2 in flight.
+  Stage s0, s1;
+  load(s0, kb);
+  if (kb + 1 < ke) load(s1, kb + 1);
+  store(s0, 0);
+  __syncthreads();
+  for (int kt = kb; kt < ke; kt += 2) {
+    if (kt + 2 < ke) load(s0, kt + 2);
+    compute(0);
+    if (kt + 1 < ke) store(s1, 1);
+    __syncthreads();
+    if (kt + 1 >= ke) break;
+    if (kt + 3 < ke) load(s1, kt + 3);
+    compute(1);
+    if (kt + 2 < ke) store(s0, 0);
     __syncthreads();
   }
 }

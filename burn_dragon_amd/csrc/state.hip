@@ -7,6 +7,9 @@
 // slow index of both x and v: v comes pre-transposed ([d][t]), and the
 // rotated x tile is written transposed into LDS ([n][t], 16-byte groups XOR
 // swizzled so that fragment reads are conflict-free).
+// Global loads run two steps ahead of the MFMAs through a two-slot register
+// ring (LDS double buffer + 2 staged steps), so a step's HBM latency is
+// covered by the two steps computed before it is needed.
 #include "bdh_bf16.h"
 
 namespace bdh {
@@ -25,6 +28,11 @@ static_assert((BK / 2) * (T256 / 8) == NT, "one x block per thread per step");
 // tile: rows n..n+7 read at distinct 16-byte bank groups.
 __device__ __forceinline__ int swz4(int n, int g) { return g ^ ((n >> 1) & 3) ^ ((n >> 3) & 3); }
 
+struct Stage {
+  uint4 ra[2], ca[2], rb[VB];
+  float wa[2];
+};
+
 template <bool ROPE>
 __global__ __launch_bounds__(NT) void state_kernel(StateArgs a) {
   const int64_t n0 = (int64_t)blockIdx.x * T256;
@@ -42,40 +50,42 @@ __global__ __launch_bounds__(NT) void state_kernel(StateArgs a) {
   const bf16_t* VT = a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.D * a.Tp;
   const float dv = a.decay ? a.decay[h] : 1.0f;
   const bool scale = a.decay != nullptr;
-
   // v columns past D are zero-filled in LDS, so partially covered waves
   // compute zeros there; waves with no column below D skip the MFMAs.
   const bool active = d0 + wn * 128 < a.D;
 
   // x block of this thread: tokens 2*tp, 2*tp+1 of the step, neurons 8*nv..
   const int tp = tid & 15, nv = tid >> 4;
-  uint4 ra[2], ca[2], rbv[VB];
-  float wa[2];
-  auto load = [&](int kt) {
+  const bool kt_partial = (a.L % BK) != 0;  // last step runs past the interval
+  auto load = [&](Stage& S, int kt) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      // tokens past the interval: load a valid row, then zero the values
+      // Tokens past the interval re-read the last valid row; their weight
+      // is 0, applied when the step is written to LDS (a select on the
+      // loaded value here would make the load wait).
       const int64_t tl = (int64_t)kt * BK + 2 * tp + i;
       const int64_t tlc = tl < a.L ? tl : a.L - 1;
       const int64_t n = n0 + nv * 8;
-      const uint4 xv = ldg16(X + tlc * a.N + n);
-      ra[i] = tl < a.L ? xv : make_uint4(0, 0, 0, 0);
-      if (ROPE) ca[i] = ldg16(CS + tlc * half + n / 2);
-      wa[i] = scale ? powf(dv, (float)(a.L - tl)) : 1.0f;
+      S.ra[i] = ldg16(X + tlc * a.N + n);
+      if (ROPE) S.ca[i] = ldg16(CS + tlc * half + n / 2);
+      S.wa[i] = tl < a.L ? (scale ? powf(dv, (float)(a.L - tl)) : 1.0f) : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < VB; ++i) {
+      // v columns past D re-read the last column: they only feed output
+      // columns that are never written.
       const int v = tid + i * NT;
       const int dd = v >> 2, kv = v & 3;
       const int64_t d = d0 + dd;
-      rbv[i] = d < a.D ? ldg16(VT + d * a.Tp + a.t0 + (int64_t)kt * BK + kv * 8)
-                       : make_uint4(0, 0, 0, 0);
+      const int64_t dc = d < a.D ? d : a.D - 1;
+      S.rb[i] = ldg16(VT + dc * a.Tp + a.t0 + (int64_t)kt * BK + kv * 8);
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](const Stage& S, int buf) {
     float v0[8], v1[8];
-    prep8_f32<ROPE>(ra[0], ca[0], wa[0], scale, v0);
-    prep8_f32<ROPE>(ra[1], ca[1], wa[1], scale, v1);
+    const bool masked = scale || kt_partial;
+    prep8_f32<ROPE>(S.ra[0], S.ca[0], S.wa[0], masked, v0);
+    prep8_f32<ROPE>(S.ra[1], S.ca[1], S.wa[1], masked, v1);
     const int tt = 2 * tp;  // even token of the pair; both share a 16-byte group
     uint32_t* Aw = reinterpret_cast<uint32_t*>(As[buf]);
 #pragma unroll
@@ -87,7 +97,7 @@ __global__ __launch_bounds__(NT) void state_kernel(StateArgs a) {
     for (int i = 0; i < VB; ++i) {
       const int v = tid + i * NT;
       const int dd = v >> 2, kv = v & 3;
-      *reinterpret_cast<uint4*>(&Bs[buf][dd * LDP + kv * 8]) = rbv[i];
+      *reinterpret_cast<uint4*>(&Bs[buf][dd * LDP + kv * 8]) = S.rb[i];
     }
   };
 
@@ -97,15 +107,10 @@ __global__ __launch_bounds__(NT) void state_kernel(StateArgs a) {
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = zero16();
 
-  const int nk = (int)((a.L + BK - 1) / BK);
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load(kt + 1);
+  auto compute = [&](int buf) {
+    if (!active) return;
 #pragma unroll
-    for (int kk = 0; kk < BK / 16 && active; ++kk) {
+    for (int kk = 0; kk < BK / 16; ++kk) {
       const int g = kk * 2 + (lane >> 5);
       bf16x8 af[2], bfr[4];
 #pragma unroll
@@ -120,10 +125,27 @@ __global__ __launch_bounds__(NT) void state_kernel(StateArgs a) {
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
-          acc[mi][ni] = mfma32(af[mi], bfr[ni], acc[mi][ni]);
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32(af[mi], bfr[ni], acc[mi][ni]);
     }
-    if (kt + 1 < nk) store(buf ^ 1);
+  };
+
+  // Pipeline: LDS holds step kt (buffer kt & 1); the register ring holds
+  // steps kt+1 and kt+2 in flight.
+  const int nk = (int)((a.L + BK - 1) / BK);
+  Stage s0, s1;
+  load(s0, 0);
+  if (nk > 1) load(s1, 1);
+  store(s0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    if (kt + 2 < nk) load(s0, kt + 2);
+    compute(0);
+    if (kt + 1 < nk) store(s1, 1);
+    __syncthreads();
+    if (kt + 1 >= nk) break;
+    if (kt + 3 < nk) load(s1, kt + 3);
+    compute(1);
+    if (kt + 2 < nk) store(s0, 0);
     __syncthreads();
   }
 
