@@ -5,19 +5,23 @@
 
 namespace bdh {
 
-// Tile geometry of the 256x256 gram / state kernels: 8 waves (2 per SIMD),
-// each owning a 64x128 block of the tile (2 x 4 MFMA 32x32 accumulators).
+// Score-block (gram) and state tiles are 256 x 256.
 constexpr int T256 = 256;
-constexpr int T256_THREADS = 512;
-constexpr int T256_BK = 32;                // k step
-constexpr int T256_LDP = T256_BK + 8;      // padded LDS pitch (bf16), 80 B rows
 
 __device__ __forceinline__ uint4 ldg16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
+// 16-byte load at a wave-uniform base plus a 32-bit per-lane byte offset: the
+// base stays in SGPRs and no 64-bit address math is done per lane.
+__device__ __forceinline__ uint4 ldg16_off(const void* base, uint32_t byte_off) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + byte_off);
+}
 
 // (even, odd) bf16 pair rotated by the packed bf16 (cos, sin) word csw:
-//   re = e*c - o*s = dot2((e,o), (c,-s)) ; ro = e*s + o*c = dot2((e,o), (s,c))
+//   re = e*c - o*s = dot2((e, o), (c, -s)) ; ro = e*s + o*c = dot2((e, o), (s, c))
+// Through the compiler builtin only: written as inline assembly, a
+// v_dot2_f32_bf16 result read two instructions later came back stale on
+// gfx950 (the compiler cannot see the instruction's latency there).
 __device__ __forceinline__ void rot_pair(uint32_t xw, uint32_t csw, float& re, float& ro) {
   const bf16x2 xv = __builtin_bit_cast(bf16x2, xw);
   const bf16x2 cms = __builtin_bit_cast(bf16x2, csw ^ 0x80000000u);
@@ -64,26 +68,39 @@ __device__ __forceinline__ float decay_pow(const float* decay, int64_t h, float 
   return decay ? powf(decay[h], e) : 1.0f;
 }
 
-// --- launch interfaces ---------------------------------------------------------
-struct GramArgs {
-  const bf16_t* x;
-  const uint32_t* cs;   // packed bf16 (cos, sin) [T, N/2] or null
+// --- launch interface of the gram + state kernel (mfma_prefill.hip) --------
+// One launch runs two kinds of work unit, heaviest first:
+//   gram units  (stream, N range kp, interval iv, 256-row x 128-column tile
+//               touching the interval's lower triangle): part[kp, s, iv] =
+//               the tile of tril(-1)(Q Q^T * d^(r-c)) summed over the kp-th
+//               N range;
+//   state units (stream, 128-neuron block, 256-column block) of the
+//               interval [st_t0, st_t0 + st_Lc):
+//               rho_out = rho_in * d^Lc + (Q * d^(Lc-r))^T V.
+// Either kind may be absent (gram_ids == 0 or state_units == 0).
+struct PrefillArgs {
+  const bf16_t* x;      // [S, T, N]
+  const uint32_t* cs;   // packed bf16 (cos, sin) [T, N/2], or null (x pre-rotated)
+  const float* decay;   // [H] or null
+  int64_t H, Hv, T, N, D, S;
+  // gram units
   float* part;          // [KS, S, n_iv, Lp, Lp]
-  const float* decay;
-  int64_t H, T, N, L, Lp, S, n_iv;
-  int ks, tiles_per_iv;
+  int64_t L, Lp, n_iv;
+  int ks, nb;           // N splits (N/32 a multiple of 4 ks); 256-row blocks per interval
+  int gram_groups;      // S * ks * n_iv
+  int gram_ids;         // workgroup ids reserved for gram units (prefill_gram_ids)
+  // state units
+  const bf16_t* vt;     // [B*Hv, Dp, Tp], zero past (D, T); Dp = D rounded up to 256
+  const float* rho_in;  // [S, N, D] or null
+  float* rho_out;       // [S, N, D]
+  int64_t st_t0, st_Lc, Tp, Dp;  // Tp >= st_t0 + st_Lc rounded up to 128
+  int state_units;      // prefill_state_units(S, N, D), or 0
 };
-hipError_t launch_gram(const GramArgs& g, bool rope, hipStream_t st);
-
-struct StateArgs {
-  const bf16_t* x;
-  const uint32_t* cs;
-  const bf16_t* vt;   // [B*Hv, D, Tp]
-  const float* rho_in;
-  float* rho_out;
-  const float* decay;
-  int64_t H, Hv, T, N, D, t0, L, Tp, S;
-};
-hipError_t launch_state(const StateArgs& a, bool rope, hipStream_t st);
+hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
+// Workgroup ids a gram launch needs for `groups` groups of nb-block
+// intervals (ids are laid out so that one group's tiles share an XCD).
+int prefill_gram_ids(int groups, int nb);
+// State units of one interval.
+int prefill_state_units(int64_t S, int64_t N, int64_t D);
 
 }  // namespace bdh

@@ -62,6 +62,17 @@ __device__ __forceinline__ floatx16 mfma32(const bf16x8& a, const bf16x8& b, con
 __device__ __forceinline__ int acc_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 __device__ __forceinline__ int acc_col(int lane) { return lane & 31; }
 
+// --- MFMA 16x16x32 bf16 (gfx950) ---------------------------------------------
+// Operand fragments (8 bf16 per lane): lane l covers row/col (l & 15) and
+// k = 8*(l >> 4) .. +7 of the 32-deep slice.  Accumulator (4 f32 per lane):
+// col = l & 15, row = 4*(l >> 4) + r.
+__device__ __forceinline__ floatx4 mfma16(const bf16x8& a, const bf16x8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ int acc16_row(int lane, int r) { return 4 * (lane >> 4) + r; }
+__device__ __forceinline__ int acc16_col(int lane) { return lane & 15; }
+__device__ __forceinline__ floatx4 zero4() { return floatx4{0.0f, 0.0f, 0.0f, 0.0f}; }
+
 // Wavefront index within the workgroup as a scalar (SGPR) value, so that
 // branches on it are uniform scalar branches rather than exec-mask ones.
 __device__ __forceinline__ int wave_id() {

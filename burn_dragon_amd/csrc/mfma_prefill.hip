@@ -1,0 +1,344 @@
+// Gram and state products of the bf16 chunked prefill (gfx950 MFMA), in one
+// launch.  Each workgroup computes a 256x128 (gram) or 128x256 (state)
+// output tile of a bf16 product with fp32 accumulation: 4 waves, each owning
+// a 64x128 block of v_mfma_f32_16x16x32_bf16 accumulators (128 AGPRs).  Two
+// workgroups share a CU (61 KB of LDS and 256 registers per lane each), so
+// while one waits on its loads, rotates its next tile or synchronises, the
+// other's MFMAs keep the matrix cores busy.
+//
+//   gram unit   S_kp[r, c] = sum_{n in range kp} q_r[n] q_c[n] for one
+//               256-row x 128-column tile touching an interval's lower
+//               triangle, written (masked to c < r, times d^(r-c)) to the
+//               partial buffer kp; contraction over neurons.  Waves whose 64
+//               rows lie wholly above the diagonal skip the MFMAs.
+//   state unit  rho_out[n, d] = rho_in[n, d] * d^Lc + sum_t q_t[n] d^(Lc-t) v_t[d]
+//               for a 128-neuron x 256-column block; contraction over tokens,
+//               so the rotated x tile is written transposed ([n][t]) to LDS.
+//
+// q = RoPE(x) is applied between HBM and LDS from the packed bf16 (cos, sin)
+// table.  K steps are 32 deep; LDS holds two steps (double buffer) and the
+// global loads of step k+1 are in flight while step k is multiplied.  Every
+// unit runs an even number of steps (the host guarantees it), so the step
+// loop has a single exit; with a mid-loop exit the compiler moves the
+// accumulators between AGPRs and VGPRs on every iteration.
+// Units are ordered heaviest first (gram tiles, then state blocks), so the
+// state units' HBM-bound rho writes fill the tail of the MFMA-bound gram work.
+#include "bdh_bf16.h"
+
+namespace bdh {
+namespace {
+
+constexpr int NT = 256;               // 4 waves
+constexpr int BK = 32;                // k step: 64-byte LDS rows of four 16-byte chunks
+constexpr int ROWS = T256 + T256 / 2; // operand rows per step (256 + 128)
+constexpr int BUF = ROWS * BK;        // bf16 elements of one step's operands
+
+// Element offset of 16-byte chunk c (0..3) of LDS row r.  Chunks are XOR
+// swizzled with bits 1..2 of the row: measured on gfx950 (LDS bank-conflict
+// counter), this makes both the MFMA fragment reads (16 rows x 4 chunks per
+// wave) and the row-segment writes (4 lanes per row) conflict-free, where a
+// padded 80-byte pitch has 2x conflicts on each.
+__device__ __forceinline__ int lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 3)) << 3); }
+
+__device__ __forceinline__ bf16x8 frag(const bf16_t* base, int row, int lane) {
+  return *reinterpret_cast<const bf16x8*>(&base[lds_off(row + (lane & 15), lane >> 4)]);
+}
+
+// acc[mi][ni] += A[arow + 16 mi] x B[brow + 16 ni]^T over one 32-deep step
+// (rows of both operands k-contiguous): 4 x 8 MFMAs.  All 12 fragments are
+// requested up front, in the order the MFMAs consume them, so the first
+// MFMAs wait only for the first reads and one LDS round trip covers the step.
+__device__ __forceinline__ void mma_64x128(const bf16_t* A, const bf16_t* B, int lane, int arow,
+                                           int brow, floatx4 (&acc)[4][8]) {
+  bf16x8 af[4], bfr[8];
+  af[0] = frag(A, arow, lane);
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) bfr[ni] = frag(B, brow + ni * 16, lane);
+#pragma unroll
+  for (int mi = 1; mi < 4; ++mi) af[mi] = frag(A, arow + mi * 16, lane);
+#pragma unroll
+  for (int ni = 4; ni < 8; ++ni) bfr[ni] = frag(B, brow + ni * 16, lane);
+#pragma unroll
+  for (int nh = 0; nh < 2; ++nh)
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+        acc[mi][nh * 4 + ni] = mfma16(af[mi], bfr[nh * 4 + ni], acc[mi][nh * 4 + ni]);
+}
+
+__device__ __forceinline__ void zero_acc(floatx4 (&acc)[4][8]) {
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = zero4();
+}
+
+// Steps [kb, ke), an even count: LDS buffer (kt - kb) & 1 holds step kt; the
+// loads of step kt+1 are issued before step kt's MFMAs and written to the
+// other buffer after them.
+template <class Load, class Store, class Compute>
+__device__ __forceinline__ void run_steps(int kb, int ke, Load&& load, Store&& store,
+                                          Compute&& compute) {
+  load(kb);
+  store(0);
+  __syncthreads();
+  for (int kt = kb; kt < ke; kt += 2) {
+    load(kt + 1);
+    compute(0);
+    store(1);
+    __syncthreads();
+    if (kt + 2 < ke) load(kt + 2);
+    compute(1);
+    if (kt + 2 < ke) store(0);
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gram unit: rows ri .. ri+255 (A) x columns rj .. rj+127 (B) of interval iv,
+// N range [kb, ke) in BK steps.
+template <bool ROPE, bool DECAY, bool WHOLE>
+__device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int64_t s, int kp,
+                                          int64_t iv, int64_t ri, int64_t rj) {
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int64_t t0 = iv * a.L;
+  const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
+  const int64_t rowb = a.N * 2;  // bytes per x row, and per table row (N/2 words)
+  const char* X = reinterpret_cast<const char*>(a.x + (s * a.T + t0) * a.N);
+  const char* CS = ROPE ? reinterpret_cast<const char*>(a.cs + t0 * (a.N / 2)) : nullptr;
+  const int nk = (int)(a.N / BK);
+  const int kb = (int)((int64_t)nk * kp / a.ks), ke = (int)((int64_t)nk * (kp + 1) / a.ks);
+
+  // Loader: 4 lanes per 64-byte row segment; group g < 4 covers A rows
+  // rb + 64 g, g = 4, 5 cover B rows rb + 64 (g - 4).  WHOLE tiles (inside
+  // the interval) use uniform row bases and one per-lane offset.  Tiles that
+  // cross the end of a ragged interval re-read its last row for the rows past
+  // it: their scores are never written (and a select on the loaded value
+  // would stall the load).
+  const int kc = tid & 3, rb = tid >> 2;
+  const uint32_t lane_off = (uint32_t)(rb * rowb + kc * 16);
+  struct Stage {
+    uint4 xr[6], cr[6];
+  } st;
+  auto load = [&](int kt) {
+    const int64_t kofs = (int64_t)kt * 64;  // 32 bf16 of x, 16 words of the table
+#pragma unroll
+    for (int g = 0; g < 6; ++g) {
+      const int64_t r0 = (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
+      if (WHOLE) {
+        const int64_t o = r0 * rowb + kofs;
+        st.xr[g] = ldg16_off(X + o, lane_off);
+        if (ROPE) st.cr[g] = ldg16_off(CS + o, lane_off);
+      } else {
+        const int64_t t = r0 + rb;
+        const uint32_t o = (uint32_t)((t < Lc ? t : Lc - 1) * rowb + kc * 16);
+        st.xr[g] = ldg16_off(X + kofs, o);
+        if (ROPE) st.cr[g] = ldg16_off(CS + kofs, o);
+      }
+    }
+  };
+  auto store = [&](int buf) {
+    bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
+#pragma unroll
+    for (int g = 0; g < 6; ++g)
+      *reinterpret_cast<uint4*>(&base[lds_off(64 * g + rb, kc)]) = prep8<ROPE>(st.xr[g], st.cr[g], 1.0f, false);
+  };
+
+  floatx4 acc[4][8];
+  zero_acc(acc);
+  // Waves whose 64 rows end at or before the tile's first column compute
+  // nothing that is kept; nor do waves starting past a ragged interval.
+  const bool active = ri + 64 * w + 64 > rj + 1 && ri + 64 * w < Lc;
+  run_steps(kb, ke, load, store, [&](int buf) {
+    if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + T256 * BK, lane, 64 * w, 0, acc);
+  });
+
+  if (!active) return;
+  const float l2d = DECAY ? log2f(a.decay[s % a.H]) : 0.0f;
+  float* P = a.part + (((int64_t)kp * a.S + s) * a.n_iv + iv) * a.Lp * a.Lp;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t ti = ri + 64 * w + mi * 16 + acc16_row(lane, r);
+        const int64_t tj = rj + ni * 16 + acc16_col(lane);
+        if (ti < Lc && tj < Lc) {
+          const float v = acc[mi][ni][r];
+          P[ti * a.Lp + tj] = tj < ti ? (DECAY ? v * exp2f((float)(ti - tj) * l2d) : v) : 0.0f;
+        }
+      }
+}
+
+// ---------------------------------------------------------------------------
+// state unit: rho block (n0 .. n0+127, d0 .. d0+255) of stream s over tokens
+// [st_t0, st_t0 + st_Lc).
+template <bool ROPE, bool DECAY, bool WHOLE>
+__device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, int64_t s,
+                                           int64_t n0, int64_t d0) {
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int wm = w >> 1, wn = w & 1;  // n rows 64*wm.., d cols 128*wn..
+  const int64_t b = s / a.H, h = s - b * a.H;
+  const int64_t t0 = a.st_t0, Lc = a.st_Lc;
+  const int64_t rowb = a.N * 2;  // bytes per x row and per table row
+  const char* X = reinterpret_cast<const char*>(a.x + s * a.T * a.N);
+  const char* CS = reinterpret_cast<const char*>(a.cs);
+  const char* VT = reinterpret_cast<const char*>(a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp);
+  const float l2d = DECAY ? log2f(a.decay[h]) : 0.0f;  // d^e = exp2(e log2 d)
+
+  // x loader: lane block of 2 tokens (2 tp, 2 tp + 1) x 8 neurons (8 nv ..).
+  // In a unit whose steps run past T (ragged last interval, !WHOLE), tokens
+  // past T re-read row T-1: their v^T columns are zero-padded, so they add 0.
+  const int tp = tid & 15, nv = tid >> 4;
+  const uint32_t xlane = (uint32_t)(2 * tp * rowb + (n0 + 8 * nv) * 2);
+  // v^T loader: 4 lanes per 64-byte segment of a row d, rows vb + 64 i (v^T
+  // has Dp = D rounded up to 256 rows, zero past D).
+  const int kc = tid & 3, vb = tid >> 2;
+  const int64_t vrow = a.Tp * 2;
+  const uint32_t vlane = (uint32_t)(vb * vrow + kc * 16);
+  struct Stage {
+    uint4 xr[2], cr[2], vr[4];
+  } st;
+  int cur = 0;
+  auto load = [&](int kt) {
+    cur = kt;
+    const int64_t tb = t0 + (int64_t)kt * BK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (WHOLE) {
+        const int64_t o = (tb + i) * rowb;
+        st.xr[i] = ldg16_off(X + o, xlane);
+        if (ROPE) st.cr[i] = ldg16_off(CS + o, xlane);
+      } else {
+        const int64_t t = tb + 2 * tp + i;
+        const uint32_t o = (uint32_t)((t < a.T ? t : a.T - 1) * rowb + (n0 + 8 * nv) * 2);
+        st.xr[i] = ldg16_off(X, o);
+        if (ROPE) st.cr[i] = ldg16_off(CS, o);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.vr[i] = ldg16_off(VT + (d0 + 64 * i) * vrow + tb * 2, vlane);
+  };
+  auto store = [&](int buf) {
+    bf16_t* A = lds + buf * BUF;             // [n][t], 128 rows
+    bf16_t* B = lds + buf * BUF + 128 * BK;  // [d][t], 256 rows
+    float f0[8], f1[8];
+    float w0 = 1.0f, w1 = 1.0f;
+    if (DECAY) {
+      const int64_t tl = (int64_t)cur * BK + 2 * tp;
+      w0 = tl < Lc ? exp2f((float)(Lc - tl) * l2d) : 0.0f;
+      w1 = tl + 1 < Lc ? exp2f((float)(Lc - tl - 1) * l2d) : 0.0f;
+    }
+    prep8_f32<ROPE>(st.xr[0], st.cr[0], w0, DECAY, f0);
+    prep8_f32<ROPE>(st.xr[1], st.cr[1], w1, DECAY, f1);
+    uint32_t* Aw = reinterpret_cast<uint32_t*>(A);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      Aw[(lds_off(8 * nv + e, tp >> 2) + 2 * (tp & 3)) >> 1] = pack_bf16x2(f0[e], f1[e]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&B[lds_off(vb + 64 * i, kc)]) = st.vr[i];
+  };
+
+  floatx4 acc[4][8];
+  zero_acc(acc);
+  const bool active = d0 + wn * 128 < a.D;
+  const int nk = (int)(((Lc + 63) / 64) * 2);  // even; steps past Lc read zero v columns
+  run_steps(0, nk, load, store, [&](int buf) {
+    if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + 128 * BK, lane, 64 * wm, 128 * wn, acc);
+  });
+
+  // Columns past D (zero v^T rows) are computed and never written.
+  const float carry = DECAY ? exp2f((float)Lc * l2d) : 1.0f;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t n = n0 + 64 * wm + mi * 16 + acc16_row(lane, r);
+        const int64_t d = d0 + 128 * wn + ni * 16 + acc16_col(lane);
+        if (d < a.D) {
+          const int64_t idx = (s * a.N + n) * a.D + d;
+          const float prev = a.rho_in ? a.rho_in[idx] * carry : 0.0f;
+          a.rho_out[idx] = prev + acc[mi][ni][r];
+        }
+      }
+}
+
+// ---------------------------------------------------------------------------
+// Gram tiles of one interval: 256-row block rb (of nb) x 128-column block cb,
+// for every cb < 2 (rb + 1); tile u enumerates them row block by row block.
+// Gram ids: blocks of 8 groups; inside a block, id = tile * 8 + (group & 7),
+// so the tiles of one group (which read the same x rows) have ids congruent
+// mod 8 and run on one XCD (the dispatcher sends id i to XCD i % 8).
+__device__ __forceinline__ void tile_of(int u, int& rbk, int& cbk) {
+  rbk = 0;
+  while ((rbk + 1) * (rbk + 2) <= u) ++rbk;
+  cbk = u - rbk * (rbk + 1);
+}
+
+template <bool ROPE, bool DECAY>
+__global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * BUF];
+  const int id = blockIdx.x;
+  if (id < a.gram_ids) {
+    const int tpg = a.nb * (a.nb + 1);
+    const int blk = id / (8 * tpg), rem = id - blk * 8 * tpg;
+    const int u = rem >> 3;
+    const int g = blk * 8 + (rem & 7);
+    if (g >= a.gram_groups) return;
+    const int64_t iv = g % a.n_iv;
+    const int q = (int)(g / a.n_iv);
+    const int kp = q % a.ks;
+    const int64_t s = q / a.ks;
+    int rbk, cbk;
+    tile_of(u, rbk, cbk);
+    const int64_t t0 = iv * a.L;
+    const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
+    const int64_t ri = (int64_t)rbk * T256, rj = (int64_t)cbk * (T256 / 2);
+    if (ri >= Lc || rj >= Lc) return;  // tile past a ragged last interval: never read
+    if (ri + T256 <= Lc) gram_unit<ROPE, DECAY, true>(a, lds, s, kp, iv, ri, rj);
+    else gram_unit<ROPE, DECAY, false>(a, lds, s, kp, iv, ri, rj);
+  } else {
+    const int sid = id - a.gram_ids;
+    if (sid >= a.state_units) return;
+    const int nt = (int)(a.N / (T256 / 2));
+    const int dt = (int)((a.D + T256 - 1) / T256);
+    const int64_t s = sid / (nt * dt);
+    const int rem = sid - (int)s * nt * dt;
+    const int64_t n0 = (int64_t)(rem / dt) * (T256 / 2), d0 = (int64_t)(rem % dt) * T256;
+    // Steps cover round_up(Lc, 64) tokens; they stay inside T unless the
+    // interval is a ragged last one.
+    if (a.st_t0 + ((a.st_Lc + 63) / 64) * 64 <= a.T) state_unit<ROPE, DECAY, true>(a, lds, s, n0, d0);
+    else state_unit<ROPE, DECAY, false>(a, lds, s, n0, d0);
+  }
+}
+
+}  // namespace
+
+int prefill_gram_ids(int groups, int nb) {
+  const int tpg = nb * (nb + 1);
+  return ((groups + 7) / 8) * 8 * tpg;
+}
+
+int prefill_state_units(int64_t S, int64_t N, int64_t D) {
+  return (int)(S * (N / (T256 / 2)) * ((D + T256 - 1) / T256));
+}
+
+hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st) {
+  const unsigned grid = (unsigned)(a.gram_ids + a.state_units);
+  if (grid == 0) return hipSuccess;
+  const bool decay = a.decay != nullptr;
+  if (rope) {
+    if (decay) hipLaunchKernelGGL((prefill_mfma_kernel<true, true>), dim3(grid), dim3(NT), 0, st, a);
+    else hipLaunchKernelGGL((prefill_mfma_kernel<true, false>), dim3(grid), dim3(NT), 0, st, a);
+  } else {
+    if (decay) hipLaunchKernelGGL((prefill_mfma_kernel<false, true>), dim3(grid), dim3(NT), 0, st, a);
+    else hipLaunchKernelGGL((prefill_mfma_kernel<false, false>), dim3(grid), dim3(NT), 0, st, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace bdh

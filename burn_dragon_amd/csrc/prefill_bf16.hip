@@ -35,7 +35,7 @@ struct CtxArgs {
   const float* rho;
   const float* decay;
   float* ctx;
-  int64_t H, Hv, T, N, D, t0, L, Lp, Tp, S, n_iv, iv;
+  int64_t H, Hv, T, N, D, t0, L, Lp, Tp, Dp, S, n_iv, iv;
   int ks;
 };
 
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int64_t b = s / a.H, h = s - b * a.H;
-  const bf16_t* VT = a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.D * a.Tp;
+  const bf16_t* VT = a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp;
   const int64_t pstride = a.S * a.n_iv * a.Lp * a.Lp;
   const float* P0 = a.part + (s * a.n_iv + a.iv) * a.Lp * a.Lp;
   const int64_t ecol = e0 + wave * 64;  // this wave's 64 output columns
@@ -207,10 +207,10 @@ __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
       }
 }
 
-// vt[bv, d, t] = v[bv, t, d] for t < T, 0 for T <= t < Tp.
+// vt[bv, d, t] = v[bv, t, d] for t < T, d < D; 0 for T <= t < Tp or D <= d < Dp.
 __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restrict__ v,
                                                           bf16_t* __restrict__ vt, int64_t T,
-                                                          int64_t D, int64_t Tp) {
+                                                          int64_t D, int64_t Tp, int64_t Dp) {
   __shared__ bf16_t tile[32][33];
   const int64_t bv = blockIdx.z;
   const int64_t t0 = (int64_t)blockIdx.x * 32, d0 = (int64_t)blockIdx.y * 32;
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restri
   __syncthreads();
   for (int r = ty; r < 32; r += 8) {
     const int64_t d = d0 + r, t = t0 + tx;
-    if (d < D && t < Tp) vt[(bv * D + d) * Tp + t] = tile[tx][r];
+    if (d < Dp && t < Tp) vt[(bv * Dp + d) * Tp + t] = tile[tx][r];
   }
 }
 
@@ -257,27 +257,62 @@ bool bf16_shape_supported(int64_t N, int64_t D, const char** why) {
   return true;
 }
 
+// Compute units of the current device (256 on MI355X), cached per device.
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) {
+  // The MFMA kernels address one stream's x, its RoPE table rows and one
+  // v^T slab with 32-bit byte offsets.
+  if (a.T * a.N * 2 >= (int64_t)1 << 31 || a.D * (a.T + 64) * 2 >= (int64_t)1 << 31)
+    return fail(BDH_UNSUPPORTED, "bf16 MFMA path needs time * latent < 2^30 per stream");
   const int64_t S = a.B * a.H;
   const int64_t half = a.N / 2;
-  const int64_t Tp = ((a.T + BK - 1) / BK) * BK;
+  // v^T: tokens padded to a multiple of 128 (a state unit's steps cover its
+  // interval rounded up to 128 tokens), columns to a multiple of 256 (whole
+  // 256-row tiles).
+  const int64_t Tp = ((a.T + 127) / 128) * 128;
+  const int64_t Dp = ((a.D + T256 - 1) / T256) * T256;
   const int64_t L = a.L;
   const int64_t n_iv = (a.T + L - 1) / L;
   const int64_t Lc0 = a.T < L ? a.T : L;
   const int64_t Lp = ((Lc0 + T256 - 1) / T256) * T256;
   const int nb = (int)(Lp / T256);
-  const int tiles_per_iv = nb * (nb + 1) / 2;
-  // Split the gram along N until there are ~1.5 workgroups per CU; every
-  // extra split writes (and ctx re-reads) one more partial score buffer.
-  const int64_t tiles = tiles_per_iv * n_iv * S;
-  int ks = (int)((384 + tiles - 1) / tiles);
-  const int nk = (int)(a.N / T256_BK);
-  if (ks > 8) ks = 8;
-  if (ks > nk) ks = nk;
-  if (ks < 1) ks = 1;
+  const int nk = (int)(a.N / 32);  // 32-deep gram steps
+  const int state_units = prefill_state_units(S, a.N, a.D);
+
+  // The first interval's state units share the gram launch unless the call
+  // is in place: then they would overwrite rho_in before the context kernel
+  // reads it, so they run after it.
+  const bool merge_state = a.state && !(a.rho_in && a.rho_in == a.rho_out);
+
+  // N splits of the gram: the fewest for which the longest gram unit stays
+  // within ~85% of the launch's average work per CU (one workgroup per CU;
+  // every split writes, and the context kernel re-reads, one more partial
+  // score buffer).  Work is counted in 32-deep steps of one 256x128 tile; a
+  // state unit costs its token steps plus ~4 for its rho write.
+  const double gram_work = (double)S * n_iv * nb * (nb + 1) * nk;
+  const double state_work = merge_state ? state_units * (((Lc0 + 127) / 128) * 4 + 4.0) : 0.0;
+  const double per_cu = (gram_work + state_work) / device_cus();
+  // Every N range must be a multiple of 4 steps (nk is a multiple of 8, so
+  // ks = 1 and 2 always qualify).
+  int ks = 1;
+  for (int cand = 1; cand <= 8 && nk % (4 * cand) == 0; cand *= 2) {
+    ks = cand;
+    if ((double)nk / cand <= 0.85 * per_cu) break;
+  }
 
   void *vt = nullptr, *part = nullptr, *cs = nullptr;
-  bdh_status stt = scratch(SLOT_VT, (size_t)(a.B * a.Hv * a.D * Tp) * sizeof(bf16_t), &vt);
+  bdh_status stt = scratch(SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
   if (stt != BDH_OK) return stt;
   stt = scratch(SLOT_SCORES, (size_t)(ks * S * n_iv * Lp * Lp) * sizeof(float), &part);
   if (stt != BDH_OK) return stt;
@@ -287,8 +322,8 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   }
   const bool rope = a.freqs != nullptr;
 
-  hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, 32), cdiv(a.D, 32), (unsigned)(a.B * a.Hv)),
-                     dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp);
+  hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, 32), cdiv(Dp, 32), (unsigned)(a.B * a.Hv)),
+                     dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
   uint64_t n_launch = 1;
   BDH_HIP_TRY(hipGetLastError());
   if (rope) {
@@ -298,9 +333,22 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     ++n_launch;
   }
 
-  GramArgs g{a.x, (const uint32_t*)cs, (float*)part, a.decay, a.H, a.T, a.N, L, Lp, S, n_iv,
-             ks, tiles_per_iv};
-  BDH_HIP_TRY(launch_gram(g, rope, st));
+  PrefillArgs p{};
+  p.x = a.x;
+  p.cs = (const uint32_t*)cs;
+  p.decay = a.decay;
+  p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;
+  p.part = (float*)part;
+  p.L = L; p.Lp = Lp; p.n_iv = n_iv;
+  p.ks = ks; p.nb = nb;
+  p.gram_groups = (int)(S * ks * n_iv);
+  p.gram_ids = prefill_gram_ids(p.gram_groups, nb);
+  p.vt = (const bf16_t*)vt;
+  p.rho_in = a.rho_in;
+  p.rho_out = a.rho_out;
+  p.st_t0 = 0; p.st_Lc = Lc0; p.Tp = Tp; p.Dp = Dp;
+  p.state_units = merge_state ? state_units : 0;
+  BDH_HIP_TRY(launch_prefill_mfma(p, rope, st));
   ++n_launch;
 
   const float* rho_cur = a.rho_in;
@@ -308,7 +356,7 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     const int64_t t0 = iv * L;
     const int64_t Lc = (a.T - t0 < L) ? a.T - t0 : L;
     CtxArgs c{a.x, (const uint32_t*)cs, (const bf16_t*)vt, (const float*)part, rho_cur, a.decay,
-              a.ctx, a.H, a.Hv, a.T, a.N, a.D, t0, Lc, Lp, Tp, S, n_iv, iv, ks};
+              a.ctx, a.H, a.Hv, a.T, a.N, a.D, t0, Lc, Lp, Tp, Dp, S, n_iv, iv, ks};
     const dim3 cgrid(cdiv(Lc, CTX_ROWS), cdiv(a.D, 256), (unsigned)S);
     if (rope) {
       if (rho_cur) hipLaunchKernelGGL((ctx_kernel<true, true>), cgrid, dim3(256), 0, st, c);
@@ -320,10 +368,17 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     BDH_HIP_TRY(hipGetLastError());
     ++n_launch;
     if (!a.state) continue;
-    StateArgs sa{a.x, (const uint32_t*)cs, (const bf16_t*)vt, rho_cur, a.rho_out, a.decay,
-                 a.H, a.Hv, a.T, a.N, a.D, t0, Lc, Tp, S};
-    BDH_HIP_TRY(launch_state(sa, rope, st));
-    ++n_launch;
+    if (!(iv == 0 && merge_state)) {
+      PrefillArgs q = p;
+      q.gram_ids = 0;
+      q.gram_groups = 0;
+      q.rho_in = rho_cur;
+      q.st_t0 = t0;
+      q.st_Lc = Lc;
+      q.state_units = state_units;
+      BDH_HIP_TRY(launch_prefill_mfma(q, rope, st));
+      ++n_launch;
+    }
     rho_cur = a.rho_out;
   }
   if (launches) *launches += n_launch;
