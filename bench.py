@@ -40,7 +40,8 @@ def parse():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--decode-warmup", type=int, default=4)
     ap.add_argument("--decode-prefill", type=int, default=1024, help="tokens prefilled into rho")
-    ap.add_argument("--only", choices=("all", "prefill", "decode"), default="all")
+    ap.add_argument("--only", choices=("all", "prefill", "decode", "long"), default="all")
+    ap.add_argument("--long-steps", type=int, default=3, help="timed C4 prefills")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="target CPU-baseline wall time (split between prefill and decode)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -100,6 +101,44 @@ def bench_prefill(torch, args):
                      "flop_per_launch": flop},
         "shape": {"B": B, "nh": H, "T": T, "N": N, "D": D, "chunk": C},
     }
+
+
+def bench_long(torch, args):
+    """C4: one long stream per head, T = 8192 (16 state-carry intervals)."""
+    from burn_dragon_amd import _lib
+    B, H, T, N, D, C = 1, 4, 8192, 8192, 256, 256
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(SEED + 4)
+    x = torch.relu(torch.randn(B, H, T, N, generator=g, device=dev) - 1.645).to(torch.bfloat16)
+    v = (torch.randn(B, 1, T, D, generator=g, device=dev) / 16).to(torch.bfloat16)
+    ctx = torch.empty(B, H, T, D, device=dev, dtype=torch.float32)
+    rho = torch.empty(B, H, N, D, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    plan = _lib.BdhRecurrentPlan(B, H, 1, T, N, D)
+    rope = _lib.BdhRope(_lib.BDH_ROPE_SEQUENTIAL, 0, 0, 65536.0)
+    for _ in range(2):
+        lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho)
+    torch.cuda.synchronize()
+    steps = args.long_steps
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flop = B * H * T * (4 * N * D + (C - 1) * (N + D))
+    achieved = flop / (ms * 1e-3) / 1e12
+    print(f"[long] {ms:.3f} ms/prefill, {B * T / (ms * 1e-3) / 1e6:.2f} M tok/s, "
+          f"{achieved:.1f} TFLOP/s", flush=True)
+    return {"metric": "C4 long-context prefill tokens/s per BDH layer", "value": B * T / (ms * 1e-3),
+            "unit": "tokens/s", "ms_per_prefill": ms, "steps": steps,
+            "config": {"workload": "C4 long prefill, one BDH layer: B1 nh4 T8192 N8192 D256, "
+                                   "chunk 256, bf16 in / fp32 acc, RoPE fused"},
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                         "traffic": None, "flop_per_launch": flop}}
 
 
 def bench_decode(torch, args):
@@ -272,6 +311,7 @@ def main():
 
     pre = bench_prefill(torch, args) if args.only in ("all", "prefill") else None
     dec = bench_decode(torch, args) if args.only in ("all", "decode") else None
+    lng = bench_long(torch, args) if args.only in ("all", "long") else None
 
     cpu_pre = cpu_dec = None
     if not args.no_cpu_baseline:
@@ -299,6 +339,11 @@ def main():
         if dec is not None:
             dec["cpu_baseline"] = cpu_dec
             out["decode"] = dec
+        if lng is not None:
+            out["long_prefill"] = lng
+    elif dec is None:
+        out = dict(lng, n_gpus=1, higher_is_better=True, scaling="weak", vs_baseline=None,
+                   dtype="bf16", data="synthetic")
     else:
         out = {"metric": METRIC, "value": round(dec["value"], 1), "unit": "tokens/s", "n_gpus": 1,
                "steps": dec["steps"], "warmup": dec["warmup"],

@@ -69,7 +69,7 @@ __device__ __forceinline__ float decay_pow(const float* decay, int64_t h, float 
 }
 
 // --- launch interface of the gram + state kernel (mfma_prefill.hip) --------
-// One launch runs two kinds of work unit, heaviest first:
+// One launch runs up to three kinds of work unit, heaviest first:
 //   gram units  (stream, N range kp, interval iv, 256-row x 128-column tile
 //               touching the interval's lower triangle): part[kp, s, iv] =
 //               the tile of tril(-1)(Q Q^T * d^(r-c)) summed over the kp-th
@@ -77,7 +77,10 @@ __device__ __forceinline__ float decay_pow(const float* decay, int64_t h, float 
 //   state units (stream, 128-neuron block, 256-column block) of the
 //               interval [st_t0, st_t0 + st_Lc):
 //               rho_out = rho_in * d^Lc + (Q * d^(Lc-r))^T V.
-// Either kind may be absent (gram_ids == 0 or state_units == 0).
+//   readout units (stream, 256-row block, 128-column block, N range) of
+//               the interval [rd_t0, rd_t0 + rd_Lc):
+//               rd_part[kr] = (Q * d^r) rho_iv over the kr-th N range.
+// Any kind may be absent (gram_ids, rd_units or state_units == 0).
 struct PrefillArgs {
   const bf16_t* x;      // [S, T, N]
   const uint32_t* cs;   // packed bf16 (cos, sin) [T, N/2], or null (x pre-rotated)
@@ -93,8 +96,15 @@ struct PrefillArgs {
   const bf16_t* vt;     // [B*Hv, Dp, Tp], zero past (D, T); Dp = D rounded up to 256
   const float* rho_in;  // [S, N, D] or null
   float* rho_out;       // [S, N, D]
-  int64_t st_t0, st_Lc, Tp, Dp;  // Tp >= st_t0 + st_Lc rounded up to 128
+  int64_t st_t0, st_Lc, Tp, Dp;  // Tp >= st_t0 + st_Lc rounded up to 64
   int state_units;      // prefill_state_units(S, N, D), or 0
+  // readout units: partial (Q * d^r) rho_iv for the interval
+  // [rd_t0, rd_t0 + rd_Lc), rho_iv the state at its start
+  const float* rd_rho;  // [S, N, D]
+  float* rd_part;       // [rd_kr, S, Lp, D] partials over the rd_kr N ranges
+  int64_t rd_t0, rd_Lc;
+  int rd_kr;            // N splits (N/32 a multiple of 2 rd_kr)
+  int rd_units;         // prefill_readout_units(S, rd_Lc, D, rd_kr), or 0
 };
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
 // Workgroup ids a gram launch needs for `groups` groups of nb-block
@@ -102,5 +112,7 @@ hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
 int prefill_gram_ids(int groups, int nb);
 // State units of one interval.
 int prefill_state_units(int64_t S, int64_t N, int64_t D);
+// Readout units of one interval of Lc rows.
+int prefill_readout_units(int64_t S, int64_t Lc, int64_t D, int kr);
 
 }  // namespace bdh

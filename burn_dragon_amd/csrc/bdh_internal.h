@@ -28,6 +28,9 @@ enum ScratchSlot {
   SLOT_VT,           // transposed values        [B*Hv, Dp, Tp] bf16
   SLOT_ROPE_TABLE,   // packed bf16 cos/sin per (token, pair) [T, N/2]
   SLOT_ROTATED,      // rotated queries (fp32 path) [S, T, N] f32
+  SLOT_READOUT,      // readout partials (bf16 path) [rd_kr, S, Lp, D] f32
+  SLOT_RHO_A,        // states between intervals (bf16 path) [S, N, D] f32
+  SLOT_RHO_B,
   SLOT_COUNT
 };
 bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);

@@ -14,6 +14,9 @@
 //   state unit  rho_out[n, d] = rho_in[n, d] * d^Lc + sum_t q_t[n] d^(Lc-t) v_t[d]
 //               for a 128-neuron x 256-column block; contraction over tokens,
 //               so the rotated x tile is written transposed ([n][t]) to LDS.
+//   readout unit (q_t d^t) . rho_in for 256 rows x 128 columns over one N
+//               range (split-K partial); rho is read as fp32 rows and
+//               written transposed as bf16 to LDS.
 //
 // q = RoPE(x) is applied between HBM and LDS from the packed bf16 (cos, sin)
 // table.  K steps are 32 deep; LDS holds two steps (double buffer) and the
@@ -21,8 +24,8 @@
 // unit runs an even number of steps (the host guarantees it), so the step
 // loop has a single exit; with a mid-loop exit the compiler moves the
 // accumulators between AGPRs and VGPRs on every iteration.
-// Units are ordered heaviest first (gram tiles, then state blocks), so the
-// state units' HBM-bound rho writes fill the tail of the MFMA-bound gram work.
+// Units are ordered heaviest first (gram tiles, readout blocks, then state
+// blocks), so the state units' HBM-bound rho writes fill the tail.
 #include "bdh_bf16.h"
 
 namespace bdh {
@@ -268,6 +271,98 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
 }
 
 // ---------------------------------------------------------------------------
+// readout unit: partial (Q * d^r) rho of rows r0 .. r0+255 of the interval
+// [rd_t0, rd_t0 + rd_Lc) and columns d0 .. d0+127, over the kp-th N range,
+// written to rd_part[kp].  A = the interval's rotated, decay-weighted x rows
+// (loaded as in the gram); B = rho^T, converted from the fp32 state rows and
+// written transposed ([d][n]) to LDS.
+template <bool ROPE, bool DECAY, bool WHOLE>
+__device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, int64_t s, int kp,
+                                             int64_t r0, int64_t d0) {
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int64_t t0 = a.rd_t0, Lc = a.rd_Lc;
+  const int64_t rowb = a.N * 2;  // bytes per x row, and per table row (N/2 words)
+  const char* X = reinterpret_cast<const char*>(a.x + (s * a.T + t0) * a.N);
+  const char* CS = ROPE ? reinterpret_cast<const char*>(a.cs + t0 * (a.N / 2)) : nullptr;
+  const float* R = a.rd_rho + s * a.N * a.D;
+  const int nk = (int)(a.N / BK);
+  const int kb = (int)((int64_t)nk * kp / a.rd_kr), ke = (int)((int64_t)nk * (kp + 1) / a.rd_kr);
+  const float l2d = DECAY ? log2f(a.decay[s % a.H]) : 0.0f;  // d^e = exp2(e log2 d)
+
+  // x loader (group g: rows rb + 64 g), as in the gram unit; rows past a
+  // ragged interval re-read its last row and are never stored.
+  const int kc = tid & 3, rb = tid >> 2;
+  const uint32_t lane_off = (uint32_t)(rb * rowb + kc * 16);
+  float wr[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) wr[g] = DECAY ? exp2f((float)(r0 + rb + 64 * g) * l2d) : 1.0f;
+  // rho loader: lane block of 2 state rows (2 np, 2 np + 1) x 8 columns
+  // (8 dv ..); columns past D re-read the last 8 and are never stored.
+  const int np = tid & 15, dv = tid >> 4;
+  const int64_t dcol = d0 + 8 * dv <= a.D - 8 ? d0 + 8 * dv : a.D - 8;
+  struct Stage {
+    uint4 xr[4], cr[4];
+    float4 rr[4];
+  } st;
+  auto load = [&](int kt) {
+    const int64_t kofs = (int64_t)kt * 64;  // 32 bf16 of x, 16 words of the table
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (WHOLE) {
+        const int64_t o = (r0 + 64 * g) * rowb + kofs;
+        st.xr[g] = ldg16_off(X + o, lane_off);
+        if (ROPE) st.cr[g] = ldg16_off(CS + o, lane_off);
+      } else {
+        const int64_t t = r0 + 64 * g + rb;
+        const uint32_t o = (uint32_t)((t < Lc ? t : Lc - 1) * rowb + kc * 16);
+        st.xr[g] = ldg16_off(X + kofs, o);
+        if (ROPE) st.cr[g] = ldg16_off(CS + kofs, o);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float* row = R + ((int64_t)kt * BK + 2 * np + i) * a.D + dcol;
+      st.rr[2 * i] = *reinterpret_cast<const float4*>(row);
+      st.rr[2 * i + 1] = *reinterpret_cast<const float4*>(row + 4);
+    }
+  };
+  auto store = [&](int buf) {
+    bf16_t* A = lds + buf * BUF;             // x rows 0..255
+    bf16_t* B = lds + buf * BUF + T256 * BK; // rho^T rows (columns d) 0..127
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<uint4*>(&A[lds_off(64 * g + rb, kc)]) = prep8<ROPE>(st.xr[g], st.cr[g], wr[g], DECAY);
+    const float r0v[8] = {st.rr[0].x, st.rr[0].y, st.rr[0].z, st.rr[0].w,
+                          st.rr[1].x, st.rr[1].y, st.rr[1].z, st.rr[1].w};
+    const float r1v[8] = {st.rr[2].x, st.rr[2].y, st.rr[2].z, st.rr[2].w,
+                          st.rr[3].x, st.rr[3].y, st.rr[3].z, st.rr[3].w};
+    uint32_t* Bw = reinterpret_cast<uint32_t*>(B);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      Bw[(lds_off(8 * dv + e, np >> 2) + 2 * (np & 3)) >> 1] = pack_bf16x2(r0v[e], r1v[e]);
+  };
+
+  floatx4 acc[4][8];
+  zero_acc(acc);
+  const bool active = r0 + 64 * w < Lc;
+  run_steps(kb, ke, load, store, [&](int buf) {
+    if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + T256 * BK, lane, 64 * w, 0, acc);
+  });
+  if (!active) return;
+  float* P = a.rd_part + ((int64_t)kp * a.S + s) * a.Lp * a.D;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = r0 + 64 * w + mi * 16 + acc16_row(lane, r);
+        const int64_t d = d0 + ni * 16 + acc16_col(lane);
+        if (t < Lc && d < a.D) P[t * a.D + d] = acc[mi][ni][r];
+      }
+}
+
+// ---------------------------------------------------------------------------
 // Gram tiles of one interval: 256-row block rb (of nb) x 128-column block cb,
 // for every cb < 2 (rb + 1); tile u enumerates them row block by row block.
 // Gram ids: blocks of 8 groups; inside a block, id = tile * 8 + (group & 7),
@@ -301,8 +396,21 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
     if (ri >= Lc || rj >= Lc) return;  // tile past a ragged last interval: never read
     if (ri + T256 <= Lc) gram_unit<ROPE, DECAY, true>(a, lds, s, kp, iv, ri, rj);
     else gram_unit<ROPE, DECAY, false>(a, lds, s, kp, iv, ri, rj);
+  } else if (id < a.gram_ids + a.rd_units) {
+    // readout unit: (stream, 256-row block, 128-column block, N range), N range fastest
+    int rid = id - a.gram_ids;
+    const int kp = rid % a.rd_kr;
+    rid /= a.rd_kr;
+    const int ndb = (int)((a.D + T256 / 2 - 1) / (T256 / 2));
+    const int64_t d0 = (int64_t)(rid % ndb) * (T256 / 2);
+    rid /= ndb;
+    const int nrb = (int)((a.rd_Lc + T256 - 1) / T256);
+    const int64_t r0 = (int64_t)(rid % nrb) * T256;
+    const int64_t s = rid / nrb;
+    if (r0 + T256 <= a.rd_Lc) readout_unit<ROPE, DECAY, true>(a, lds, s, kp, r0, d0);
+    else readout_unit<ROPE, DECAY, false>(a, lds, s, kp, r0, d0);
   } else {
-    const int sid = id - a.gram_ids;
+    const int sid = id - a.gram_ids - a.rd_units;
     if (sid >= a.state_units) return;
     const int nt = (int)(a.N / (T256 / 2));
     const int dt = (int)((a.D + T256 - 1) / T256);
@@ -327,8 +435,12 @@ int prefill_state_units(int64_t S, int64_t N, int64_t D) {
   return (int)(S * (N / (T256 / 2)) * ((D + T256 - 1) / T256));
 }
 
+int prefill_readout_units(int64_t S, int64_t Lc, int64_t D, int kr) {
+  return (int)(S * ((Lc + T256 - 1) / T256) * ((D + T256 / 2 - 1) / (T256 / 2)) * kr);
+}
+
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.gram_ids + a.state_units);
+  const unsigned grid = (unsigned)(a.gram_ids + a.rd_units + a.state_units);
   if (grid == 0) return hipSuccess;
   const bool decay = a.decay != nullptr;
   if (rope) {

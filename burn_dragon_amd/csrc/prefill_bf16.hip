@@ -3,18 +3,21 @@
 //
 // The sequence is split into state-carry intervals of L tokens (L a multiple
 // of the 128-token chunk).  Inside an interval the carried state of chunk c,
-// rho_c = rho_in + sum_{c'<c} Q_c'^T V_c', is applied through the chunk-pair
+// rho_c = rho_iv + sum_{c'<c} Q_c'^T V_c', is applied through the chunk-pair
 // score blocks Q_c Q_c'^T, so rho is materialised once per interval instead
-// of once per chunk:
-//   gram   S = tril(-1)(Q Q^T * d^(r-c)) for every interval (gram.hip; one
-//          launch, it does not depend on rho), split along N into KS
-//          partial buffers
-//   ctx    O = tril(S) V + (Q * d^r) rho_in   (this file; sums the partials
-//          in a fixed order, S split into bf16 hi + lo)
-//   state  rho_out = rho_in * d^L + (Q * d^(L-r))^T V   (state.hip)
+// of once per chunk.  Per interval iv (state rho_iv at its start):
+//   gram    S = tril(-1)(Q Q^T * d^(r-c)), split along N into KS partial
+//           buffers (all intervals, in the first launch: it needs no rho)
+//   readout (Q * d^r) rho_iv, split along N into rd_kr partial buffers
+//   state   rho_{iv+1} = rho_iv * d^L + (Q * d^(L-r))^T V
+//   ctx     O = tril(S) V + readout    (this file; sums the partials in a
+//           fixed order, S split into bf16 hi + lo)
+// gram, readout and state units share one launch per interval
+// (mfma_prefill.hip); the states between intervals alternate between two
+// scratch buffers and the last one lands in rho_out.
 // RoPE is applied to Q tiles between HBM and LDS from a packed bf16
 // (cos, sin) table of the call's (token, pair) phases; rotated queries are
-// never written to memory.  All products are v_mfma_f32_32x32x16_bf16.
+// never written to memory.
 #include "bdh_bf16.h"
 
 namespace bdh {
@@ -28,25 +31,22 @@ __device__ __forceinline__ int swz8(int n, int g) { return g ^ (n & 7) ^ ((n >> 
 
 // ctx: O[rows r0..r0+64, e0..e0+256] of interval iv.
 struct CtxArgs {
-  const bf16_t* x;
-  const uint32_t* cs;
   const bf16_t* vt;
-  const float* part;   // gram partials [KS, S, n_iv, Lp, Lp]
-  const float* rho;
-  const float* decay;
+  const float* part;     // gram partials [KS, S, n_iv, Lp, Lp]
+  const float* rd_part;  // readout partials [rd_kr, S, Lp, D] or null (no carried state)
   float* ctx;
-  int64_t H, Hv, T, N, D, t0, L, Lp, Tp, Dp, S, n_iv, iv;
-  int ks;
+  int64_t H, Hv, T, D, t0, L, Lp, Tp, Dp, S, n_iv, iv;
+  int ks, rd_kr;
 };
 
 constexpr int CTX_ROWS = 64;
-// LDS carve (bytes): part 1 uses Ahi, Alo [64 x LDP] and Bv [256 x LDP];
-// part 2 reuses the space for Aq [64 x LDP] and Br [256 x BK] (swizzled).
+// LDS carve (bytes): Ahi, Alo [64 x LDP] and Bv [256 x LDP].
 constexpr int CTX_A_BYTES = CTX_ROWS * LDP * 2;
 constexpr int CTX_B_BYTES = 256 * LDP * 2;
 constexpr int CTX_LDS = 2 * CTX_A_BYTES + CTX_B_BYTES;
 
-template <bool ROPE, bool HAS_RHO>
+// O = tril(S) V (+ the readout partials of the carried state, HAS_RD).
+template <bool HAS_RD>
 __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
   const int64_t r0 = (int64_t)blockIdx.x * CTX_ROWS;
   const int64_t e0 = (int64_t)blockIdx.y * 256;
@@ -132,68 +132,6 @@ __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
     __syncthreads();
   }
 
-  // ---- part 2: (Q * d^r) rho_in ----
-  if (HAS_RHO) {
-    bf16_t* Aq = Ahi;                                           // [64][LDP]
-    bf16_t* Br = reinterpret_cast<bf16_t*>(lds + CTX_A_BYTES);  // [256][BK] swizzled
-    const int64_t half = a.N / 2;
-    const bf16_t* X = a.x + (s * a.T + a.t0) * a.N;
-    const uint32_t* CS = ROPE ? a.cs + a.t0 * half : nullptr;
-    const float* R = a.rho + s * a.N * a.D;
-    const float dv = a.decay ? a.decay[h] : 1.0f;
-    const bool scale = a.decay != nullptr;
-    for (int64_t k0 = 0; k0 < a.N; k0 += BK) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int v = tid + i * 256;
-        const int m = v >> 3, kv = v & 7;
-        const int64_t row = r0 + m;
-        const bool ok = row < a.L;
-        const int64_t k = k0 + kv * 8;
-        const uint4 raw = ok ? ldg16(X + row * a.N + k) : make_uint4(0, 0, 0, 0);
-        uint4 c = make_uint4(0, 0, 0, 0);
-        if (ROPE && ok) c = ldg16(CS + row * half + k / 2);
-        const float w = scale ? powf(dv, (float)row) : 1.0f;
-        *reinterpret_cast<uint4*>(&Aq[m * LDP + kv * 8]) = prep8<ROPE>(raw, c, w, scale);
-      }
-#pragma unroll 4
-      for (int i = 0; i < 16; ++i) {
-        const int v = tid + i * 256;
-        const int l = v >> 6, e4 = v & 63;
-        const int64_t d = e0 + e4 * 4;
-        float4 rv = make_float4(0, 0, 0, 0);
-        if (d < a.D) rv = *reinterpret_cast<const float4*>(R + (k0 + l) * a.D + d);
-        const float vals[4] = {rv.x, rv.y, rv.z, rv.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int e = e4 * 4 + q;
-          Br[e * BK + swz8(e, l >> 3) * 8 + (l & 7)] = (bf16_t)vals[q];
-        }
-      }
-      __syncthreads();
-      if (wave_on) {
-#pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-          const int g = kk * 2 + (lane >> 5);
-          bf16x8 aq[2], br[2];
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi)
-            aq[mi] = *reinterpret_cast<const bf16x8*>(&Aq[(mi * 32 + (lane & 31)) * LDP + kk * 16 + 8 * (lane >> 5)]);
-#pragma unroll
-          for (int ni = 0; ni < 2; ++ni) {
-            const int e = wave * 64 + ni * 32 + (lane & 31);
-            br[ni] = *reinterpret_cast<const bf16x8*>(&Br[e * BK + swz8(e, g) * 8]);
-          }
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32(aq[mi], br[ni], acc[mi][ni]);
-        }
-      }
-      __syncthreads();
-    }
-  }
-
   float* C = a.ctx + (s * a.T + a.t0) * a.D;
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
@@ -203,7 +141,13 @@ __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int64_t row = r0 + mi * 32 + acc_row(lane, r);
         const int64_t d = ecol + ni * 32 + acc_col(lane);
-        if (row < a.L && d < a.D) C[row * a.D + d] = acc[mi][ni][r];
+        if (row < a.L && d < a.D) {
+          float v = acc[mi][ni][r];
+          if (HAS_RD) {
+            for (int kp = 0; kp < a.rd_kr; ++kp) v += a.rd_part[((kp * a.S + s) * a.Lp + row) * a.D + d];
+          }
+          C[row * a.D + d] = v;
+        }
       }
 }
 
@@ -290,28 +234,37 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   const int nk = (int)(a.N / 32);  // 32-deep gram steps
   const int state_units = prefill_state_units(S, a.N, a.D);
 
-  // The first interval's state units share the gram launch unless the call
-  // is in place: then they would overwrite rho_in before the context kernel
-  // reads it, so they run after it.
-  const bool merge_state = a.state && !(a.rho_in && a.rho_in == a.rho_out);
-
   // N splits of the gram: the fewest for which the longest gram unit stays
-  // within ~85% of the launch's average work per CU (one workgroup per CU;
-  // every split writes, and the context kernel re-reads, one more partial
-  // score buffer).  Work is counted in 32-deep steps of one 256x128 tile; a
-  // state unit costs its token steps plus ~4 for its rho write.
+  // within ~85% of the first launch's average work per workgroup slot (two
+  // per CU; every split writes, and the context kernel re-reads, one more
+  // partial score buffer).  Work is counted in 32-deep steps of one 256x128
+  // tile; a state unit costs its token steps plus ~4 for its rho write.
   const double gram_work = (double)S * n_iv * nb * (nb + 1) * nk;
-  const double state_work = merge_state ? state_units * (((Lc0 + 127) / 128) * 4 + 4.0) : 0.0;
-  const double per_cu = (gram_work + state_work) / device_cus();
-  // Every N range must be a multiple of 4 steps (nk is a multiple of 8, so
-  // ks = 1 and 2 always qualify).
+  const double state_work = a.state ? state_units * (((Lc0 + 63) / 64) * 2 + 4.0) : 0.0;
+  const double per_slot = (gram_work + state_work) / (2.0 * device_cus());
+  // Every N range must be an even number of steps (nk is a multiple of 8, so
+  // ks = 1, 2 and 4 always qualify).
   int ks = 1;
-  for (int cand = 1; cand <= 8 && nk % (4 * cand) == 0; cand *= 2) {
+  for (int cand = 1; cand <= 8 && nk % (2 * cand) == 0; cand *= 2) {
     ks = cand;
-    if ((double)nk / cand <= 0.85 * per_cu) break;
+    if ((double)nk / cand <= 0.85 * per_slot) break;
   }
 
-  void *vt = nullptr, *part = nullptr, *cs = nullptr;
+  // Readout splits: the fewest for which one readout unit stays within the
+  // average work per workgroup slot of its launch (readout + state units).
+  const bool carried = a.rho_in != nullptr || n_iv > 1;
+  int rd_kr = 1;
+  if (carried) {
+    const double rd1 = (double)prefill_readout_units(S, L, a.D, 1) * nk;
+    const double st = a.state ? state_units * (((L + 63) / 64) * 2 + 4.0) : 0.0;
+    const double slot = (rd1 + st) / (2.0 * device_cus());
+    for (int cand = 1; cand <= 8 && nk % (2 * cand) == 0; cand *= 2) {
+      rd_kr = cand;
+      if ((double)nk / cand <= 1.25 * slot) break;
+    }
+  }
+
+  void *vt = nullptr, *part = nullptr, *cs = nullptr, *rdp = nullptr, *rho_a = nullptr, *rho_b = nullptr;
   bdh_status stt = scratch(SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
   if (stt != BDH_OK) return stt;
   stt = scratch(SLOT_SCORES, (size_t)(ks * S * n_iv * Lp * Lp) * sizeof(float), &part);
@@ -319,6 +272,18 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   if (a.freqs) {
     stt = scratch(SLOT_ROPE_TABLE, (size_t)(a.T * half) * sizeof(uint32_t), &cs);
     if (stt != BDH_OK) return stt;
+  }
+  if (carried) {
+    stt = scratch(SLOT_READOUT, (size_t)(rd_kr * S * Lp * a.D) * sizeof(float), &rdp);
+    if (stt != BDH_OK) return stt;
+  }
+  if (a.state && n_iv > 1) {
+    stt = scratch(SLOT_RHO_A, (size_t)(S * a.N * a.D) * sizeof(float), &rho_a);
+    if (stt != BDH_OK) return stt;
+    if (n_iv > 2) {
+      stt = scratch(SLOT_RHO_B, (size_t)(S * a.N * a.D) * sizeof(float), &rho_b);
+      if (stt != BDH_OK) return stt;
+    }
   }
   const bool rope = a.freqs != nullptr;
 
@@ -342,44 +307,50 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   p.L = L; p.Lp = Lp; p.n_iv = n_iv;
   p.ks = ks; p.nb = nb;
   p.gram_groups = (int)(S * ks * n_iv);
-  p.gram_ids = prefill_gram_ids(p.gram_groups, nb);
   p.vt = (const bf16_t*)vt;
-  p.rho_in = a.rho_in;
-  p.rho_out = a.rho_out;
-  p.st_t0 = 0; p.st_Lc = Lc0; p.Tp = Tp; p.Dp = Dp;
-  p.state_units = merge_state ? state_units : 0;
-  BDH_HIP_TRY(launch_prefill_mfma(p, rope, st));
-  ++n_launch;
+  p.Tp = Tp; p.Dp = Dp;
+  p.rd_part = (float*)rdp;
+  p.rd_kr = rd_kr;
 
-  const float* rho_cur = a.rho_in;
+  // rho_iv for iv = 0 .. n_iv: rho_in, then the scratch buffers A, B, A, ...,
+  // and rho_out for the last.  The readout and state units of interval iv
+  // both read rho_iv; the state units write rho_{iv+1}, a different buffer
+  // except for a single in-place interval, where they run after the readout.
+  const float* cur = a.rho_in;
   for (int64_t iv = 0; iv < n_iv; ++iv) {
     const int64_t t0 = iv * L;
     const int64_t Lc = (a.T - t0 < L) ? a.T - t0 : L;
-    CtxArgs c{a.x, (const uint32_t*)cs, (const bf16_t*)vt, (const float*)part, rho_cur, a.decay,
-              a.ctx, a.H, a.Hv, a.T, a.N, a.D, t0, Lc, Lp, Tp, Dp, S, n_iv, iv, ks};
-    const dim3 cgrid(cdiv(Lc, CTX_ROWS), cdiv(a.D, 256), (unsigned)S);
-    if (rope) {
-      if (rho_cur) hipLaunchKernelGGL((ctx_kernel<true, true>), cgrid, dim3(256), 0, st, c);
-      else hipLaunchKernelGGL((ctx_kernel<true, false>), cgrid, dim3(256), 0, st, c);
-    } else {
-      if (rho_cur) hipLaunchKernelGGL((ctx_kernel<false, true>), cgrid, dim3(256), 0, st, c);
-      else hipLaunchKernelGGL((ctx_kernel<false, false>), cgrid, dim3(256), 0, st, c);
-    }
-    BDH_HIP_TRY(hipGetLastError());
+    float* next = iv == n_iv - 1 ? a.rho_out : (float*)(iv % 2 == 0 ? rho_a : rho_b);
+    const bool in_place = cur != nullptr && (const float*)next == cur;
+    p.gram_ids = iv == 0 ? prefill_gram_ids(p.gram_groups, nb) : 0;
+    p.rd_rho = cur;
+    p.rd_t0 = t0;
+    p.rd_Lc = Lc;
+    p.rd_units = cur ? prefill_readout_units(S, Lc, a.D, rd_kr) : 0;
+    p.rho_in = cur;
+    p.rho_out = next;
+    p.st_t0 = t0;
+    p.st_Lc = Lc;
+    p.state_units = (a.state && !in_place) ? state_units : 0;
+    BDH_HIP_TRY(launch_prefill_mfma(p, rope, st));
     ++n_launch;
-    if (!a.state) continue;
-    if (!(iv == 0 && merge_state)) {
+    if (a.state && in_place) {
       PrefillArgs q = p;
       q.gram_ids = 0;
-      q.gram_groups = 0;
-      q.rho_in = rho_cur;
-      q.st_t0 = t0;
-      q.st_Lc = Lc;
+      q.rd_units = 0;
       q.state_units = state_units;
       BDH_HIP_TRY(launch_prefill_mfma(q, rope, st));
       ++n_launch;
     }
-    rho_cur = a.rho_out;
+    CtxArgs c{(const bf16_t*)vt, (const float*)part, (const float*)rdp, a.ctx, a.H, a.Hv, a.T, a.D,
+              t0, Lc, Lp, Tp, Dp, S, n_iv, iv, ks, rd_kr};
+    const dim3 cgrid(cdiv(Lc, CTX_ROWS), cdiv(a.D, 256), (unsigned)S);
+    if (cur) hipLaunchKernelGGL((ctx_kernel<true>), cgrid, dim3(256), 0, st, c);
+    else hipLaunchKernelGGL((ctx_kernel<false>), cgrid, dim3(256), 0, st, c);
+    BDH_HIP_TRY(hipGetLastError());
+    ++n_launch;
+    if (!a.state) break;  // dense mode: one interval, no state
+    cur = next;
   }
   if (launches) *launches += n_launch;
   return BDH_OK;
