@@ -33,7 +33,7 @@ __device__ __forceinline__ int swz8(int n, int g) { return g ^ (n & 7) ^ ((n >> 
 struct CtxArgs {
   const bf16_t* vt;
   const float* part;     // gram partials [KS, S, n_iv, Lp, Lp]
-  const float* rd_part;  // readout partials [rd_kr, S, Lp, D] or null (no carried state)
+  const float* rd_part;  // readout partials [rd_kr, S, Lp, D] (unused here)
   float* ctx;
   int64_t H, Hv, T, D, t0, L, Lp, Tp, Dp, S, n_iv, iv;
   int ks, rd_kr;
@@ -45,8 +45,7 @@ constexpr int CTX_A_BYTES = CTX_ROWS * LDP * 2;
 constexpr int CTX_B_BYTES = 256 * LDP * 2;
 constexpr int CTX_LDS = 2 * CTX_A_BYTES + CTX_B_BYTES;
 
-// O = tril(S) V (+ the readout partials of the carried state, HAS_RD).
-template <bool HAS_RD>
+// O = tril(S) V (the readout of a carried state is added by readout_add_kernel).
 __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
   const int64_t r0 = (int64_t)blockIdx.x * CTX_ROWS;
   const int64_t e0 = (int64_t)blockIdx.y * 256;
@@ -141,14 +140,30 @@ __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int64_t row = r0 + mi * 32 + acc_row(lane, r);
         const int64_t d = ecol + ni * 32 + acc_col(lane);
-        if (row < a.L && d < a.D) {
-          float v = acc[mi][ni][r];
-          if (HAS_RD) {
-            for (int kp = 0; kp < a.rd_kr; ++kp) v += a.rd_part[((kp * a.S + s) * a.Lp + row) * a.D + d];
-          }
-          C[row * a.D + d] = v;
-        }
+        if (row < a.L && d < a.D) C[row * a.D + d] = acc[mi][ni][r];
       }
+}
+
+// ctx[s, t0 + t, :] += sum over the rd_kr readout partials (fixed order),
+// one float4 of columns per thread.
+__global__ __launch_bounds__(256) void readout_add_kernel(const float* __restrict__ rd, float* __restrict__ ctx,
+                                                          int64_t S, int64_t T, int64_t D, int64_t t0,
+                                                          int64_t Lc, int64_t Lp, int kr) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (s, t, d4)
+  const int64_t d4n = D / 4;
+  if (i >= S * Lc * d4n) return;
+  const int64_t s = i / (Lc * d4n);
+  const int64_t rem = i - s * Lc * d4n;
+  const int64_t t = rem / d4n, d = (rem - t * d4n) * 4;
+  float4 v = *reinterpret_cast<const float4*>(&ctx[(s * T + t0 + t) * D + d]);
+  for (int kp = 0; kp < kr; ++kp) {
+    const float4 r = *reinterpret_cast<const float4*>(&rd[((kp * S + s) * Lp + t) * D + d]);
+    v.x += r.x;
+    v.y += r.y;
+    v.z += r.z;
+    v.w += r.w;
+  }
+  *reinterpret_cast<float4*>(&ctx[(s * T + t0 + t) * D + d]) = v;
 }
 
 // vt[bv, d, t] = v[bv, t, d] for t < T, d < D; 0 for T <= t < Tp or D <= d < Dp.
@@ -180,9 +195,11 @@ __global__ __launch_bounds__(256) void rope_table_bf16_kernel(const float* __res
   const int64_t t = i / half;
   const int64_t k = i - t * half;
   const float p = (float)(fixed ? pos_first : pos_first + t);
-  float sn, c;
-  sincosf(rope_phase(p, freqs[2 * k]), &sn, &c);
-  cs[i] = pack_bf16x2(c, sn);
+  // frac(p f) in the reference's f32 op order; v_sin_f32 / v_cos_f32 take
+  // their argument in revolutions, so no multiply by 2 pi is needed.  Their
+  // error (~1e-6) is far below the bf16 rounding of the table.
+  const float fr = rope_frac(p, freqs[2 * k]);
+  cs[i] = pack_bf16x2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
 }
 
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
@@ -345,10 +362,15 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     CtxArgs c{(const bf16_t*)vt, (const float*)part, (const float*)rdp, a.ctx, a.H, a.Hv, a.T, a.D,
               t0, Lc, Lp, Tp, Dp, S, n_iv, iv, ks, rd_kr};
     const dim3 cgrid(cdiv(Lc, CTX_ROWS), cdiv(a.D, 256), (unsigned)S);
-    if (cur) hipLaunchKernelGGL((ctx_kernel<true>), cgrid, dim3(256), 0, st, c);
-    else hipLaunchKernelGGL((ctx_kernel<false>), cgrid, dim3(256), 0, st, c);
+    hipLaunchKernelGGL(ctx_kernel, cgrid, dim3(256), 0, st, c);
     BDH_HIP_TRY(hipGetLastError());
     ++n_launch;
+    if (cur) {
+      hipLaunchKernelGGL(readout_add_kernel, dim3(cdiv(S * Lc * (a.D / 4), 256)), dim3(256), 0, st,
+                         (const float*)rdp, a.ctx, S, a.T, a.D, t0, Lc, Lp, rd_kr);
+      BDH_HIP_TRY(hipGetLastError());
+      ++n_launch;
+    }
     if (!a.state) break;  // dense mode: one interval, no state
     cur = next;
   }
