@@ -252,22 +252,42 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
     if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + 128 * BK, lane, 64 * wm, 128 * wn, acc);
   });
 
+  // Epilogue through LDS (free after the last step's barrier): per 16-row
+  // slice mi, each wave writes its 16 x 128 fp32 block to its own region
+  // (row pitch 132 floats: the four 4-row groups of a store land in distinct
+  // banks), then stores it as 512-byte row segments of 16-byte lanes.
   // Columns past D (zero v^T rows) are computed and never written.
   const float carry = DECAY ? exp2f((float)Lc * l2d) : 1.0f;
+  constexpr int EP = 132;
+  float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
+  const int64_t dcol = d0 + 128 * wn + 4 * (lane & 31);
+  const bool dok = dcol < a.D;  // D is a multiple of 32: a float4 is all in or all out
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
     for (int ni = 0; ni < 8; ++ni)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t n = n0 + 64 * wm + mi * 16 + acc16_row(lane, r);
-        const int64_t d = d0 + 128 * wn + ni * 16 + acc16_col(lane);
-        if (d < a.D) {
-          const int64_t idx = (s * a.N + n) * a.D + d;
-          const float prev = a.rho_in ? a.rho_in[idx] * carry : 0.0f;
-          a.rho_out[idx] = prev + acc[mi][ni][r];
+      for (int r = 0; r < 4; ++r) E[acc16_row(lane, r) * EP + ni * 16 + acc16_col(lane)] = acc[mi][ni][r];
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 16; rr += 2) {
+      const int row = rr + (lane >> 5);
+      float4 v = *reinterpret_cast<const float4*>(&E[row * EP + 4 * (lane & 31)]);
+      const int64_t n = n0 + 64 * wm + mi * 16 + row;
+      const int64_t idx = (s * a.N + n) * a.D + dcol;
+      if (dok) {
+        if (a.rho_in) {
+          const float4 pv = *reinterpret_cast<const float4*>(&a.rho_in[idx]);
+          v.x += pv.x * carry;
+          v.y += pv.y * carry;
+          v.z += pv.z * carry;
+          v.w += pv.w * carry;
         }
+        *reinterpret_cast<float4*>(&a.rho_out[idx]) = v;
       }
+    }
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------

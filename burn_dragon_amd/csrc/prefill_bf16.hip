@@ -23,45 +23,109 @@
 namespace bdh {
 namespace {
 
-constexpr int BK = 64;         // k step of the context kernel
-constexpr int LDP = BK + 8;    // padded LDS pitch (bf16)
+constexpr int CK = 32;         // k step of the context kernel: 64-byte LDS rows
+constexpr int CTX_ROWS = 64;   // output rows of one workgroup
+constexpr int CTX_COLS = 256;  // output columns of one workgroup (4 waves x 64)
 
-// XOR swizzle of the 8-element groups of a 64-wide transposed tile row n.
-__device__ __forceinline__ int swz8(int n, int g) { return g ^ (n & 7) ^ ((n >> 3) & 7); }
+// Element offset of 16-byte chunk c (0..3) of a 64-byte LDS row r, XOR
+// swizzled with bits 1..2 of the row: conflict-free for MFMA fragment reads
+// (8 consecutive rows of one chunk per LDS cycle) and for row-segment writes.
+__device__ __forceinline__ int cofs(int r, int c) { return r * CK + ((c ^ ((r >> 1) & 3)) << 3); }
 
-// ctx: O[rows r0..r0+64, e0..e0+256] of interval iv.
+// O = tril(S) V for every interval in [iv0, iv0 + n_ivc) at once: S is the
+// sum of the KS gram partials of its interval, which the first prefill
+// launch writes for all intervals.  (The readout of a carried state is added
+// per interval by readout_add_kernel.)
 struct CtxArgs {
-  const bf16_t* vt;
+  const bf16_t* vt;      // [B*Hv, Dp, Tp]
   const float* part;     // gram partials [KS, S, n_iv, Lp, Lp]
-  const float* rd_part;  // readout partials [rd_kr, S, Lp, D] (unused here)
-  float* ctx;
-  int64_t H, Hv, T, D, t0, L, Lp, Tp, Dp, S, n_iv, iv;
-  int ks, rd_kr;
+  float* ctx;            // [S, T, D]
+  int64_t H, Hv, T, D, L, Lp, Tp, Dp, S, n_iv;
+  int iv0, n_ivc;        // intervals covered by this launch
+  int nrb;               // CTX_ROWS row blocks per interval: ceil(min(L, T) / 64)
 };
 
-constexpr int CTX_ROWS = 64;
-// LDS carve (bytes): Ahi, Alo [64 x LDP] and Bv [256 x LDP].
-constexpr int CTX_A_BYTES = CTX_ROWS * LDP * 2;
-constexpr int CTX_B_BYTES = 256 * LDP * 2;
-constexpr int CTX_LDS = 2 * CTX_A_BYTES + CTX_B_BYTES;
+// Workgroup id -> (row block, interval, stream): row blocks heaviest first
+// (row block rb contracts over 64 (rb + 1) columns), then interval, then
+// stream.  blockIdx.y is the 256-column block.
+template <int KS>
+__global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
+  const int nz = (int)(a.S * a.n_ivc);
+  const int id = blockIdx.x;
+  const int rb = a.nrb - 1 - id / nz;
+  const int z = id - (id / nz) * nz;
+  const int64_t iv = a.iv0 + z / a.S, s = z % a.S;
+  const int64_t t0 = iv * a.L;
+  const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
+  const int64_t r0 = (int64_t)rb * CTX_ROWS;
+  if (r0 >= Lc) return;  // a ragged last interval has fewer row blocks
+  const int64_t e0 = (int64_t)blockIdx.y * CTX_COLS;
 
-// O = tril(S) V (the readout of a carried state is added by readout_add_kernel).
-__global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
-  const int64_t r0 = (int64_t)blockIdx.x * CTX_ROWS;
-  const int64_t e0 = (int64_t)blockIdx.y * 256;
-  const int64_t s = blockIdx.z;
-  __shared__ __attribute__((aligned(16))) char lds[CTX_LDS];
-  bf16_t* Ahi = reinterpret_cast<bf16_t*>(lds);
-  bf16_t* Alo = reinterpret_cast<bf16_t*>(lds + CTX_A_BYTES);
-  bf16_t* Bv = reinterpret_cast<bf16_t*>(lds + 2 * CTX_A_BYTES);
+  __shared__ __attribute__((aligned(16))) bf16_t Ahi[CTX_ROWS * CK];
+  __shared__ __attribute__((aligned(16))) bf16_t Alo[CTX_ROWS * CK];
+  __shared__ __attribute__((aligned(16))) bf16_t Bv[CTX_COLS * CK];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int64_t b = s / a.H, h = s - b * a.H;
-  const bf16_t* VT = a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp;
+  const bf16_t* VT = a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp + t0;
   const int64_t pstride = a.S * a.n_iv * a.Lp * a.Lp;
-  const float* P0 = a.part + (s * a.n_iv + a.iv) * a.Lp * a.Lp;
+  const float* P0 = a.part + (s * a.n_iv + iv) * a.Lp * a.Lp;
   const int64_t ecol = e0 + wave * 64;  // this wave's 64 output columns
   const bool wave_on = ecol < a.D;
+  // Columns [0, kend) of the score rows r0 .. r0+63 are written by the gram
+  // (zero on and above the diagonal); past kend nothing is read.
+  const int64_t kend = (r0 + CTX_ROWS < Lc) ? r0 + CTX_ROWS : Lc;
+  const int nk = (int)((kend + CK - 1) / CK);
+
+  // Loaders.  Scores: 8 lanes per 32-column row segment (4 floats each),
+  // rows m and m + 32.  v^T: 4 lanes per 64-byte row segment, rows dv + 64 i
+  // (v^T is zero past D up to Dp, a multiple of 256, so no column test).
+  const int sm = tid >> 3, sc = tid & 7;
+  const int dv = tid >> 2, kc = tid & 3;
+  struct Stage {
+    float4 p[2][KS];
+    uint4 v[4];
+  } st;
+  auto load = [&](int kt) {
+    const int64_t k0 = (int64_t)kt * CK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t row = r0 + sm + 32 * i, col = k0 + sc * 4;
+      const bool in = row < Lc && col < kend;
+#pragma unroll
+      for (int kp = 0; kp < KS; ++kp)
+        st.p[i][kp] = in ? *reinterpret_cast<const float4*>(P0 + kp * pstride + row * a.Lp + col)
+                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.v[i] = ldg16(VT + (e0 + dv + 64 * i) * a.Tp + k0 + kc * 8);
+  };
+  auto store = [&](int kt) {
+    const int64_t k0 = (int64_t)kt * CK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float4 sv = st.p[i][0];
+#pragma unroll
+      for (int kp = 1; kp < KS; ++kp) {
+        sv.x += st.p[i][kp].x;
+        sv.y += st.p[i][kp].y;
+        sv.z += st.p[i][kp].z;
+        sv.w += st.p[i][kp].w;
+      }
+      // a step that runs past kend (ragged interval) reads zeros there
+      const int64_t col = k0 + sc * 4;
+      if (col + 1 >= kend) sv.y = 0.0f;
+      if (col + 2 >= kend) sv.z = 0.0f;
+      if (col + 3 >= kend) sv.w = 0.0f;
+      const float hx = bf16_round(sv.x), hy = bf16_round(sv.y), hz = bf16_round(sv.z), hw = bf16_round(sv.w);
+      const int o = cofs(sm + 32 * i, sc >> 1) + (sc & 1) * 4;
+      *reinterpret_cast<uint2*>(&Ahi[o]) = make_uint2(pack_bf16x2(hx, hy), pack_bf16x2(hz, hw));
+      *reinterpret_cast<uint2*>(&Alo[o]) =
+          make_uint2(pack_bf16x2(sv.x - hx, sv.y - hy), pack_bf16x2(sv.z - hz, sv.w - hw));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&Bv[cofs(dv + 64 * i, kc)]) = st.v[i];
+  };
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -69,56 +133,24 @@ __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = zero16();
 
-  // ---- part 1: tril(S) V with S = sum of the KS partials, split bf16 hi + lo
-  const int64_t kend = (r0 + CTX_ROWS < a.L) ? r0 + CTX_ROWS : a.L;
-  for (int64_t k0 = 0; k0 < kend; k0 += BK) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int v = tid + i * 256;
-      const int m = v >> 4, c4 = v & 15;
-      const int64_t row = r0 + m, col = k0 + c4 * 4;
-      float4 sv = make_float4(0, 0, 0, 0);
-      if (row < a.L && col < kend) {
-        for (int kp = 0; kp < a.ks; ++kp) {
-          const float4 pv = *reinterpret_cast<const float4*>(P0 + kp * pstride + row * a.Lp + col);
-          sv.x += pv.x;
-          sv.y += pv.y;
-          sv.z += pv.z;
-          sv.w += pv.w;
-        }
-        // columns >= kend lie outside the written score blocks
-        if (col + 1 >= kend) sv.y = 0.0f;
-        if (col + 2 >= kend) sv.z = 0.0f;
-        if (col + 3 >= kend) sv.w = 0.0f;
-      }
-      const float hx = bf16_round(sv.x), hy = bf16_round(sv.y), hz = bf16_round(sv.z), hw = bf16_round(sv.w);
-      const uint2 hv = make_uint2(pack_bf16x2(hx, hy), pack_bf16x2(hz, hw));
-      const uint2 lv = make_uint2(pack_bf16x2(sv.x - hx, sv.y - hy), pack_bf16x2(sv.z - hz, sv.w - hw));
-      *reinterpret_cast<uint2*>(&Ahi[m * LDP + c4 * 4]) = hv;
-      *reinterpret_cast<uint2*>(&Alo[m * LDP + c4 * 4]) = lv;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int v = tid + i * 256;
-      const int dd = v >> 3, kv = v & 7;
-      const int64_t d = e0 + dd;
-      const uint4 val = d < a.D ? ldg16(VT + d * a.Tp + a.t0 + k0 + kv * 8) : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(&Bv[dd * LDP + kv * 8]) = val;
-    }
+  load(0);
+  for (int kt = 0; kt < nk; ++kt) {
+    store(kt);
     __syncthreads();
+    if (kt + 1 < nk) load(kt + 1);
     if (wave_on) {
 #pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
-        const int ko = kk * 16 + 8 * (lane >> 5);
+      for (int kk = 0; kk < CK / 16; ++kk) {
+        const int c = 2 * kk + (lane >> 5);
         bf16x8 ah[2], al[2], bv[2];
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
-          ah[mi] = *reinterpret_cast<const bf16x8*>(&Ahi[(mi * 32 + (lane & 31)) * LDP + ko]);
-          al[mi] = *reinterpret_cast<const bf16x8*>(&Alo[(mi * 32 + (lane & 31)) * LDP + ko]);
+          ah[mi] = *reinterpret_cast<const bf16x8*>(&Ahi[cofs(mi * 32 + (lane & 31), c)]);
+          al[mi] = *reinterpret_cast<const bf16x8*>(&Alo[cofs(mi * 32 + (lane & 31), c)]);
         }
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni)
-          bv[ni] = *reinterpret_cast<const bf16x8*>(&Bv[(wave * 64 + ni * 32 + (lane & 31)) * LDP + ko]);
+          bv[ni] = *reinterpret_cast<const bf16x8*>(&Bv[cofs(wave * 64 + ni * 32 + (lane & 31), c)]);
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -131,7 +163,8 @@ __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
     __syncthreads();
   }
 
-  float* C = a.ctx + (s * a.T + a.t0) * a.D;
+  if (!wave_on) return;
+  float* C = a.ctx + (s * a.T + t0) * a.D;
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -140,8 +173,20 @@ __global__ __launch_bounds__(256) void ctx_kernel(CtxArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int64_t row = r0 + mi * 32 + acc_row(lane, r);
         const int64_t d = ecol + ni * 32 + acc_col(lane);
-        if (row < a.L && d < a.D) C[row * a.D + d] = acc[mi][ni][r];
+        if (row < Lc && d < a.D) C[row * a.D + d] = acc[mi][ni][r];
       }
+}
+
+hipError_t launch_ctx(const CtxArgs& c, int ks, hipStream_t st) {
+  const dim3 grid((unsigned)(c.nrb * c.S * c.n_ivc), (unsigned)((c.D + CTX_COLS - 1) / CTX_COLS));
+  switch (ks) {
+    case 1: hipLaunchKernelGGL(ctx_kernel<1>, grid, dim3(256), 0, st, c); break;
+    case 2: hipLaunchKernelGGL(ctx_kernel<2>, grid, dim3(256), 0, st, c); break;
+    case 4: hipLaunchKernelGGL(ctx_kernel<4>, grid, dim3(256), 0, st, c); break;
+    case 8: hipLaunchKernelGGL(ctx_kernel<8>, grid, dim3(256), 0, st, c); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 // ctx[s, t0 + t, :] += sum over the rd_kr readout partials (fixed order),
@@ -359,12 +404,14 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
       BDH_HIP_TRY(launch_prefill_mfma(q, rope, st));
       ++n_launch;
     }
-    CtxArgs c{(const bf16_t*)vt, (const float*)part, (const float*)rdp, a.ctx, a.H, a.Hv, a.T, a.D,
-              t0, Lc, Lp, Tp, Dp, S, n_iv, iv, ks, rd_kr};
-    const dim3 cgrid(cdiv(Lc, CTX_ROWS), cdiv(a.D, 256), (unsigned)S);
-    hipLaunchKernelGGL(ctx_kernel, cgrid, dim3(256), 0, st, c);
-    BDH_HIP_TRY(hipGetLastError());
-    ++n_launch;
+    if (iv == 0) {
+      // tril(S) V of every interval: the gram partials are all written by
+      // the first launch.
+      CtxArgs c{(const bf16_t*)vt, (const float*)part, a.ctx, a.H, a.Hv, a.T, a.D, L, Lp, Tp, Dp, S,
+                n_iv, 0, (int)(a.state ? n_iv : 1), (int)cdiv(Lc0, CTX_ROWS)};
+      BDH_HIP_TRY(launch_ctx(c, ks, st));
+      ++n_launch;
+    }
     if (cur) {
       hipLaunchKernelGGL(readout_add_kernel, dim3(cdiv(S * Lc * (a.D / 4), 256)), dim3(256), 0, st,
                          (const float*)rdp, a.ctx, S, a.T, a.D, t0, Lc, Lp, rd_kr);
