@@ -17,40 +17,84 @@ __device__ __forceinline__ uint4 ldg16_off(const void* base, uint32_t byte_off) 
   return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + byte_off);
 }
 
-// (even, odd) bf16 pair rotated by the packed bf16 (cos, sin) word csw:
-//   re = e*c - o*s = dot2((e, o), (c, -s)) ; ro = e*s + o*c = dot2((e, o), (s, c))
-// Through the compiler builtin only: written as inline assembly, a
-// v_dot2_f32_bf16 result read two instructions later came back stale on
-// gfx950 (the compiler cannot see the instruction's latency there).
-__device__ __forceinline__ void rot_pair(uint32_t xw, uint32_t csw, float& re, float& ro) {
-  const bf16x2 xv = __builtin_bit_cast(bf16x2, xw);
-  const bf16x2 cms = __builtin_bit_cast(bf16x2, csw ^ 0x80000000u);
-  const bf16x2 sc = __builtin_bit_cast(bf16x2, __builtin_amdgcn_alignbit(csw, csw, 16));
-  re = __builtin_amdgcn_fdot2_f32_bf16(xv, cms, 0.0f, false);
-  ro = __builtin_amdgcn_fdot2_f32_bf16(xv, sc, 0.0f, false);
+// RoPE rotation of 4 (even, odd) bf16 pairs x.{x,y,z,w} by the packed bf16
+// (cos, sin) words cs.{x,y,z,w}:
+//   re = e*c - o*s = (e, o) . (c, s) with the high product negated (neg_hi)
+//   ro = o*c + e*s = (o, e) . (c, s), (o, e) = x rotated by 16 bits
+// Written in assembly for the three-operand v_dot2_f32_bf16 and its neg_hi
+// modifier (4 VALU instructions a pair; the builtin selects v_dot2c, which
+// needs a zeroed accumulator copy and an explicit negation, 7 a pair).  The
+// hardware needs 3 wait states between a v_dot2 that writes a VGPR and
+// another VALU instruction that reads it, and the compiler cannot see inside
+// the assembly, so every such read below is at least 3 instructions (with
+// the s_nop, 5) after its write, and the f32 form ends with s_nop 2.  Results
+// match the builtin dot product bit for bit (fp32 dot, round to nearest even
+// on packing).
+__device__ __forceinline__ uint4 rot8_bf16(uint4 x, uint4 cs) {
+  uint4 o;
+  float t0, t1, t2, t3, t4, t5, t6, t7;
+  uint32_t w0, w1, w2, w3;
+  asm("v_alignbit_b32 %12, %16, %16, 16\n\t"
+      "v_alignbit_b32 %13, %17, %17, 16\n\t"
+      "v_alignbit_b32 %14, %18, %18, 16\n\t"
+      "v_alignbit_b32 %15, %19, %19, 16\n\t"
+      "v_dot2_f32_bf16 %4, %16, %20, 0 neg_hi:[0,1,0]\n\t"
+      "v_dot2_f32_bf16 %5, %12, %20, 0\n\t"
+      "v_dot2_f32_bf16 %6, %17, %21, 0 neg_hi:[0,1,0]\n\t"
+      "v_dot2_f32_bf16 %7, %13, %21, 0\n\t"
+      "v_dot2_f32_bf16 %8, %18, %22, 0 neg_hi:[0,1,0]\n\t"
+      "v_dot2_f32_bf16 %9, %14, %22, 0\n\t"
+      "v_dot2_f32_bf16 %10, %19, %23, 0 neg_hi:[0,1,0]\n\t"
+      "v_dot2_f32_bf16 %11, %15, %23, 0\n\t"
+      "s_nop 1\n\t"
+      "v_cvt_pk_bf16_f32 %0, %4, %5\n\t"
+      "v_cvt_pk_bf16_f32 %1, %6, %7\n\t"
+      "v_cvt_pk_bf16_f32 %2, %8, %9\n\t"
+      "v_cvt_pk_bf16_f32 %3, %10, %11"
+      : "=v"(o.x), "=v"(o.y), "=v"(o.z), "=v"(o.w), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3),
+        "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7), "=&v"(w0), "=&v"(w1), "=&v"(w2), "=&v"(w3)
+      : "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w), "v"(cs.x), "v"(cs.y), "v"(cs.z), "v"(cs.w));
+  return o;
+}
+
+// Same rotation, results left in f32: out[2p] = re, out[2p + 1] = ro of pair p.
+__device__ __forceinline__ void rot8_f32(uint4 x, uint4 cs, float (&out)[8]) {
+  uint32_t w0, w1, w2, w3;
+  asm("v_alignbit_b32 %8, %12, %12, 16\n\t"
+      "v_alignbit_b32 %9, %13, %13, 16\n\t"
+      "v_alignbit_b32 %10, %14, %14, 16\n\t"
+      "v_alignbit_b32 %11, %15, %15, 16\n\t"
+      "v_dot2_f32_bf16 %0, %12, %16, 0 neg_hi:[0,1,0]\n\t"
+      "v_dot2_f32_bf16 %1, %8, %16, 0\n\t"
+      "v_dot2_f32_bf16 %2, %13, %17, 0 neg_hi:[0,1,0]\n\t"
+      "v_dot2_f32_bf16 %3, %9, %17, 0\n\t"
+      "v_dot2_f32_bf16 %4, %14, %18, 0 neg_hi:[0,1,0]\n\t"
+      "v_dot2_f32_bf16 %5, %10, %18, 0\n\t"
+      "v_dot2_f32_bf16 %6, %15, %19, 0 neg_hi:[0,1,0]\n\t"
+      "v_dot2_f32_bf16 %7, %11, %19, 0\n\t"
+      "s_nop 2"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]),
+        "=&v"(out[6]), "=&v"(out[7]), "=&v"(w0), "=&v"(w1), "=&v"(w2), "=&v"(w3)
+      : "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w), "v"(cs.x), "v"(cs.y), "v"(cs.z), "v"(cs.w));
 }
 
 // 8 bf16 (4 pairs) rotated (ROPE) and/or scaled by w, as f32.
 template <bool ROPE>
 __device__ __forceinline__ void prep8_f32(uint4 raw, uint4 cs, float w, bool scale,
                                           float (&out)[8]) {
-  const uint32_t in[4] = {raw.x, raw.y, raw.z, raw.w};
-  const uint32_t c[4] = {cs.x, cs.y, cs.z, cs.w};
+  if (ROPE) {
+    rot8_f32(raw, cs, out);
+  } else {
+    const uint32_t in[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    float re, ro;
-    if (ROPE) {
-      rot_pair(in[p], c[p], re, ro);
-    } else {
-      re = bf16_lo(in[p]);
-      ro = bf16_hi(in[p]);
+    for (int p = 0; p < 4; ++p) {
+      out[2 * p] = bf16_lo(in[p]);
+      out[2 * p + 1] = bf16_hi(in[p]);
     }
-    if (scale) {
-      re *= w;
-      ro *= w;
-    }
-    out[2 * p] = re;
-    out[2 * p + 1] = ro;
+  }
+  if (scale) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] *= w;
   }
 }
 
@@ -58,6 +102,7 @@ __device__ __forceinline__ void prep8_f32(uint4 raw, uint4 cs, float w, bool sca
 template <bool ROPE>
 __device__ __forceinline__ uint4 prep8(uint4 raw, uint4 cs, float w, bool scale) {
   if (!ROPE && !scale) return raw;
+  if (ROPE && !scale) return rot8_bf16(raw, cs);
   float v[8];
   prep8_f32<ROPE>(raw, cs, w, scale, v);
   return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),

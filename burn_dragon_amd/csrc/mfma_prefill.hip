@@ -77,6 +77,34 @@ __device__ __forceinline__ void zero_acc(floatx4 (&acc)[4][8]) {
     for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = zero4();
 }
 
+// Epilogue of a wave's 64 x 128 fp32 accumulator block, through LDS (free
+// once the step loop's last barrier has passed): per 16-row slice mi the
+// wave writes its block to its own region (row pitch 132 floats, so the four
+// 4-row groups of one store land in distinct banks) and reads it back as
+// rows, two per instruction, 16 bytes per lane; emit(row, col, v) receives
+// row 0..63 and column 0..124 (a multiple of 4) of the block.  Every wave
+// of the workgroup must call it (it holds barriers).
+template <class Emit>
+__device__ __forceinline__ void epilogue_64x128(const floatx4 (&acc)[4][8], bf16_t* lds, int w,
+                                                int lane, Emit&& emit) {
+  constexpr int EP = 132;
+  float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) E[acc16_row(lane, r) * EP + ni * 16 + acc16_col(lane)] = acc[mi][ni][r];
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 16; rr += 2) {
+      const int row = rr + (lane >> 5), col = 4 * (lane & 31);
+      emit(mi * 16 + row, col, *reinterpret_cast<const float4*>(&E[row * EP + col]));
+    }
+    __syncthreads();
+  }
+}
+
 // Steps [kb, ke), an even count: LDS buffer (kt - kb) & 1 holds step kt; the
 // loads of step kt+1 are issued before step kt's MFMAs and written to the
 // other buffer after them.
@@ -157,22 +185,27 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
     if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + T256 * BK, lane, 64 * w, 0, acc);
   });
 
-  if (!active) return;
+  // Scores of rows ti < Lc and columns tj < Lc: times d^(ti - tj) below
+  // the diagonal, 0 on and above it.  Waves that computed nothing still
+  // take part in the epilogue's barriers.
   const float l2d = DECAY ? log2f(a.decay[s % a.H]) : 0.0f;
   float* P = a.part + (((int64_t)kp * a.S + s) * a.n_iv + iv) * a.Lp * a.Lp;
+  epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
+    const int64_t ti = ri + 64 * w + row, tj = rj + col;
+    if (!active || ti >= Lc) return;
+    float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+    for (int j = 0; j < 4; ++j)
+      e[j] = tj + j < ti ? (DECAY ? e[j] * exp2f((float)(ti - tj - j) * l2d) : e[j]) : 0.0f;
+    float* dst = P + ti * a.Lp + tj;
+    if (tj + 3 < Lc) {
+      *reinterpret_cast<float4*>(dst) = make_float4(e[0], e[1], e[2], e[3]);
+    } else {
 #pragma unroll
-    for (int ni = 0; ni < 8; ++ni)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t ti = ri + 64 * w + mi * 16 + acc16_row(lane, r);
-        const int64_t tj = rj + ni * 16 + acc16_col(lane);
-        if (ti < Lc && tj < Lc) {
-          const float v = acc[mi][ni][r];
-          P[ti * a.Lp + tj] = tj < ti ? (DECAY ? v * exp2f((float)(ti - tj) * l2d) : v) : 0.0f;
-        }
-      }
+      for (int j = 0; j < 4; ++j)
+        if (tj + j < Lc) dst[j] = e[j];
+    }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -252,42 +285,22 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
     if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + 128 * BK, lane, 64 * wm, 128 * wn, acc);
   });
 
-  // Epilogue through LDS (free after the last step's barrier): per 16-row
-  // slice mi, each wave writes its 16 x 128 fp32 block to its own region
-  // (row pitch 132 floats: the four 4-row groups of a store land in distinct
-  // banks), then stores it as 512-byte row segments of 16-byte lanes.
-  // Columns past D (zero v^T rows) are computed and never written.
+  // Columns past D (zero v^T rows) are computed and never written; D is a
+  // multiple of 32, so a float4 of columns is all in or all out.
   const float carry = DECAY ? exp2f((float)Lc * l2d) : 1.0f;
-  constexpr int EP = 132;
-  float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
-  const int64_t dcol = d0 + 128 * wn + 4 * (lane & 31);
-  const bool dok = dcol < a.D;  // D is a multiple of 32: a float4 is all in or all out
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-    for (int ni = 0; ni < 8; ++ni)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) E[acc16_row(lane, r) * EP + ni * 16 + acc16_col(lane)] = acc[mi][ni][r];
-    __syncthreads();
-#pragma unroll
-    for (int rr = 0; rr < 16; rr += 2) {
-      const int row = rr + (lane >> 5);
-      float4 v = *reinterpret_cast<const float4*>(&E[row * EP + 4 * (lane & 31)]);
-      const int64_t n = n0 + 64 * wm + mi * 16 + row;
-      const int64_t idx = (s * a.N + n) * a.D + dcol;
-      if (dok) {
-        if (a.rho_in) {
-          const float4 pv = *reinterpret_cast<const float4*>(&a.rho_in[idx]);
-          v.x += pv.x * carry;
-          v.y += pv.y * carry;
-          v.z += pv.z * carry;
-          v.w += pv.w * carry;
-        }
-        *reinterpret_cast<float4*>(&a.rho_out[idx]) = v;
-      }
+  epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
+    const int64_t n = n0 + 64 * wm + row, d = d0 + 128 * wn + col;
+    if (d >= a.D) return;
+    const int64_t idx = (s * a.N + n) * a.D + d;
+    if (a.rho_in) {
+      const float4 pv = *reinterpret_cast<const float4*>(&a.rho_in[idx]);
+      v.x += pv.x * carry;
+      v.y += pv.y * carry;
+      v.z += pv.z * carry;
+      v.w += pv.w * carry;
     }
-    __syncthreads();
-  }
+    *reinterpret_cast<float4*>(&a.rho_out[idx]) = v;
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -368,18 +381,11 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
   run_steps(kb, ke, load, store, [&](int buf) {
     if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + T256 * BK, lane, 64 * w, 0, acc);
   });
-  if (!active) return;
   float* P = a.rd_part + ((int64_t)kp * a.S + s) * a.Lp * a.D;
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 8; ++ni)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t t = r0 + 64 * w + mi * 16 + acc16_row(lane, r);
-        const int64_t d = d0 + ni * 16 + acc16_col(lane);
-        if (t < Lc && d < a.D) P[t * a.D + d] = acc[mi][ni][r];
-      }
+  epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
+    const int64_t t = r0 + 64 * w + row, d = d0 + col;
+    if (t < Lc && d < a.D) *reinterpret_cast<float4*>(&P[t * a.D + d]) = v;
+  });
 }
 
 // ---------------------------------------------------------------------------
