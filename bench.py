@@ -31,6 +31,17 @@ PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 SEED = 20260729
 
+# HBM-side bytes per launch of each leg's measured unit, from rocprofv3
+# FETCH_SIZE and WRITE_SIZE runs of this script (one counter per run), each
+# scaled by what the counter reads for a 1 GiB device copy (--only copy):
+# FETCH_SIZE x 2.0, WRITE_SIZE x 1.0.  Commands and per-kernel figures:
+# profiles/prefill_c2_traffic.txt, profiles/decode_c3_traffic.txt,
+# profiles/long_prefill_c4_traffic.txt.  Counters cannot run inside this
+# process, so the figures are recorded here; they change when the kernels do.
+TRAFFIC_PREFILL_C2 = 1198.9e6   # prefill pass (transpose, table, prefill launch, ctx)
+TRAFFIC_DECODE_C3 = 428.0e6     # one decode_kernel launch
+TRAFFIC_LONG_C4 = 5010.9e6      # one C4 prefill call (34 launches)
+
 
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -40,7 +51,9 @@ def parse():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--decode-warmup", type=int, default=4)
     ap.add_argument("--decode-prefill", type=int, default=1024, help="tokens prefilled into rho")
-    ap.add_argument("--only", choices=("all", "prefill", "decode", "long"), default="all")
+    ap.add_argument("--only", choices=("all", "prefill", "decode", "long", "copy"), default="all",
+                    help="one leg only; 'copy' times a 1 GiB device copy (the calibration kernel "
+                         "of the FETCH_SIZE / WRITE_SIZE counter runs)")
     ap.add_argument("--long-steps", type=int, default=3, help="timed C4 prefills")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="target CPU-baseline wall time (split between prefill and decode)")
@@ -96,8 +109,9 @@ def bench_prefill(torch, args):
         "flop": flop,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None,
-                     "kernel": "prefill pass: gram_bf16 + ctx_bf16 + state_bf16 (+ rope table, V transpose)",
+                     "traffic": TRAFFIC_PREFILL_C2,
+                     "kernel": "prefill pass: prefill_mfma_kernel (gram + state units) + ctx_kernel "
+                               "(+ rope table, V transpose), timed as one unit",
                      "flop_per_launch": flop},
         "shape": {"B": B, "nh": H, "T": T, "N": N, "D": D, "chunk": C},
     }
@@ -138,7 +152,7 @@ def bench_long(torch, args):
                                    "chunk 256, bf16 in / fp32 acc, RoPE fused"},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                         "traffic": None, "flop_per_launch": flop}}
+                         "traffic": TRAFFIC_LONG_C4, "flop_per_launch": flop}}
 
 
 def bench_decode(torch, args):
@@ -214,7 +228,7 @@ def bench_decode(torch, args):
                    f"[64,4,8192,256] prefilled by {P} tokens, {K} steps, RoPE at the step position"},
         "active_fraction": round(frac_active, 5),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_DECODE_C3,
                      "kernel": "decode_kernel", "bytes_per_launch": round(bytes_per_step)},
     }
 
@@ -292,6 +306,28 @@ def cpu_baseline_decode(target_s: float):
                       f"op-sequence step over all N*D of rho, {t_total:.2f} s wall"}
 
 
+def bench_copy(torch):
+    """A plain 1 GiB device-to-device copy: the known-size kernel against which
+    the FETCH_SIZE / WRITE_SIZE counters are scaled (a copy reads and writes
+    exactly 1 GiB)."""
+    n = 1 << 28
+    a = torch.ones(n, device="cuda", dtype=torch.float32)
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 5
+    print(json.dumps({"copy_bytes": 4 * n, "ms": round(ms, 4),
+                      "read_plus_write_GBs": round(2 * 4 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
 # --------------------------------------------------------------------------- #
 def main():
     args = parse()
@@ -309,6 +345,9 @@ def main():
         print("device is not gfx950", file=sys.stderr)
         sys.exit(2)
 
+    if args.only == "copy":
+        bench_copy(torch)
+        return
     pre = bench_prefill(torch, args) if args.only in ("all", "prefill") else None
     dec = bench_decode(torch, args) if args.only in ("all", "decode") else None
     lng = bench_long(torch, args) if args.only in ("all", "long") else None
