@@ -76,19 +76,34 @@ __global__ __launch_bounds__(DR_THREADS) void decode_kernel(DecodeKernelArgs p) 
       const int base = seg0 + tid * DR_ROWS_PER_THREAD;
       float r[DR_ROWS_PER_THREAD];
       unsigned m = 0;
+      // A thread's 8 rows hold 4 whole (even, odd) pairs.  With N a multiple
+      // of 8 they are one aligned 32-byte block of x (and of the
+      // frequencies): two 16-byte loads each instead of 24 scalar loads.
+      float xv[DR_ROWS_PER_THREAD], fv[DR_ROWS_PER_THREAD];
+      const bool blk = (p.N & 7) == 0 && base < seg_end &&
+                       ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.freqs)) & 15) == 0;
+      if (blk) {
+        *reinterpret_cast<float4*>(&xv[0]) = *reinterpret_cast<const float4*>(xs + base);
+        *reinterpret_cast<float4*>(&xv[4]) = *reinterpret_cast<const float4*>(xs + base + 4);
+        if (ROPE) {
+          *reinterpret_cast<float4*>(&fv[0]) = *reinterpret_cast<const float4*>(p.freqs + base);
+          *reinterpret_cast<float4*>(&fv[4]) = *reinterpret_cast<const float4*>(p.freqs + base + 4);
+        }
+      }
 #pragma unroll
       for (int e = 0; e < DR_ROWS_PER_THREAD; ++e) {
         const int i = base + e;
         r[e] = 0.0f;
         if (i < seg_end) {
-          const float xi = xs[i];
+          const float xi = blk ? xv[e] : xs[i];
           bool on;
           if (ROPE) {
-            const float xp = xs[i ^ 1];
-            on = xi != 0.0f || (xp != 0.0f && rope_frac(p.pos, p.freqs[i]) != 0.0f);
+            const float xp = blk ? xv[e ^ 1] : xs[i ^ 1];
+            const float fi = blk ? fv[e] : p.freqs[i];
+            on = xi != 0.0f || (xp != 0.0f && rope_frac(p.pos, fi) != 0.0f);
             if (on) {
               float sn, cs, ev, od;
-              sincosf(rope_phase(p.pos, p.freqs[i]), &sn, &cs);
+              sincosf(rope_phase(p.pos, fi), &sn, &cs);
               if ((i & 1) == 0) rope_pair_exact(xi, xp, cs, sn, ev, od), r[e] = ev;
               else rope_pair_exact(xp, xi, cs, sn, ev, od), r[e] = od;
             }
