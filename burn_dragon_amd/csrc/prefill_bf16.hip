@@ -320,7 +320,7 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     const double rd1 = (double)prefill_readout_units(S, L, a.D, 1) * nk;
     const double st = a.state ? state_units * (((L + 63) / 64) * 2 + 4.0) : 0.0;
     const double slot = (rd1 + st) / (2.0 * device_cus());
-    for (int cand = 1; cand <= 8 && nk % (2 * cand) == 0; cand *= 2) {
+    for (int cand = 1; cand <= 16 && nk % (2 * cand) == 0; cand *= 2) {
       rd_kr = cand;
       if ((double)nk / cand <= 1.25 * slot) break;
     }
