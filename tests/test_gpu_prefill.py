@@ -114,6 +114,7 @@ def _bf16_case(rng, B, H, Hv, T, N, D, with_rho):
     (1, 2, 2, 300, 256, 96, True, None, 17),          # ragged T, per-head V, rho_in
     (1, 2, 1, 1100, 256, 128, True, None, 3),         # 3 state intervals (512+512+76)
     (1, 4, 1, 256, 256, 64, True, [0.99, 0.98, 0.97, 0.96], 0),  # ALiBi-style decay
+    (1, 2, 1, 700, 512, 320, True, [0.995, 0.99], 9),  # D > 256, not a multiple of 256; 2 intervals
 ])
 def test_bf16_rope_prefill_matches_oracle(oracle, B, H, Hv, T, N, D, with_rho, decay, pos):
     torch = need_gpu()
