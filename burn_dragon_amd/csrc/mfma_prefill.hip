@@ -147,6 +147,12 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   // cross the end of a ragged interval re-read its last row for the rows past
   // it: their scores are never written (and a select on the loaded value
   // would stall the load).
+  // A tile whose 128 columns are tokens of its own 256 rows (rj - ri = 0 or
+  // 128) takes its B operand from the A rows already in LDS: groups 4 and 5
+  // load nothing.  The row offset is a multiple of 8, so a row's swizzle is
+  // the same seen from either base.
+  const bool inner = rj >= ri && rj + T256 / 2 <= ri + T256;
+  const int groups = inner ? 4 : 6;
   const int kc = tid & 3, rb = tid >> 2;
   const uint32_t lane_off = (uint32_t)(rb * rowb + kc * 16);
   struct Stage {
@@ -156,6 +162,7 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
     const int64_t kofs = (int64_t)kt * 64;  // 32 bf16 of x, 16 words of the table
 #pragma unroll
     for (int g = 0; g < 6; ++g) {
+      if (g >= groups) break;
       const int64_t r0 = (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
       if (WHOLE) {
         const int64_t o = r0 * rowb + kofs;
@@ -172,8 +179,10 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   auto store = [&](int buf) {
     bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
 #pragma unroll
-    for (int g = 0; g < 6; ++g)
+    for (int g = 0; g < 6; ++g) {
+      if (g >= groups) break;
       *reinterpret_cast<uint4*>(&base[lds_off(64 * g + rb, kc)]) = prep8<ROPE>(st.xr[g], st.cr[g], 1.0f, false);
+    }
   };
 
   floatx4 acc[4][8];
@@ -181,8 +190,9 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   // Waves whose 64 rows end at or before the tile's first column compute
   // nothing that is kept; nor do waves starting past a ragged interval.
   const bool active = ri + 64 * w + 64 > rj + 1 && ri + 64 * w < Lc;
+  const int brow = inner ? (int)(rj - ri) : T256;  // LDS row of the first B row
   run_steps(kb, ke, load, store, [&](int buf) {
-    if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + T256 * BK, lane, 64 * w, 0, acc);
+    if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF, lane, 64 * w, brow, acc);
   });
 
   // Scores of rows ti < Lc and columns tj < Lc: times d^(ti - tj) below
