@@ -35,6 +35,10 @@ class BdhRecurrentPlan(ctypes.Structure):
                 ("batch", "heads", "value_heads", "time", "latent", "embd")]
 
 
+class BdhLayerPlan(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in ("batch", "heads", "time", "latent", "embd")]
+
+
 class BdhProfileSnapshot(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in (
         "calls", "launches", "total_ns", "setup_ns", "copy_ns", "dispatch_ns",
@@ -59,6 +63,9 @@ SIGNATURES = {
                                             _vp]),
     "bdh_dense_causal_attention_fwd": (_i32, [ctypes.POINTER(BdhRecurrentPlan), _i32, _vp, _vp,
                                               _vp, _vp, _vp]),
+    "bdh_lowrank_pack_weights": (_i32, [_i64] * 3 + [_vp] * 7),
+    "bdh_lowrank_layer_fwd": (_i32, [ctypes.POINTER(BdhLayerPlan), _vp, _vp, _vp, _vp,
+                                     ctypes.POINTER(BdhRope), _vp, _vp, _vp]),
     "bdh_profile_enable": (None, [_i32]),
     "bdh_profile_reset": (None, []),
     "bdh_profile_get": (None, [ctypes.POINTER(BdhProfileSnapshot)]),

@@ -333,6 +333,73 @@ bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads, in
   return st;
 }
 
+bdh_status bdh_lowrank_pack_weights(int64_t heads, int64_t latent, int64_t embd,
+                                    const float* encoder, const float* encoder_v,
+                                    const float* decoder, void* encoder_packed,
+                                    void* encoder_v_packed, void* decoder_packed,
+                                    void* stream) {
+  ProfScope prof;
+  if (heads <= 0 || latent <= 0 || embd <= 0) return fail(BDH_UNSUPPORTED, "zero-sized dimension");
+  if (!encoder || !encoder_v || !decoder || !encoder_packed || !encoder_v_packed || !decoder_packed)
+    return fail(BDH_EINVAL, "null tensor pointer");
+  if (heads * latent > (int64_t)32 * kMaxGrid) return fail(BDH_UNSUPPORTED, "heads * latent too large");
+  if (heads > kMaxGrid) return fail(BDH_UNSUPPORTED, "heads exceeds 65535");
+  bdh_status st = pack_lowrank_weights(heads, latent, embd, encoder, encoder_v, decoder,
+                                       (bf16_t*)encoder_packed, (bf16_t*)encoder_v_packed,
+                                       (bf16_t*)decoder_packed, (hipStream_t)stream);
+  if (st != BDH_OK) return st;
+  prof.launches = 3;
+  prof.done(true);
+  return BDH_OK;
+}
+
+bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* current,
+                                 const void* encoder_packed, const void* encoder_v_packed,
+                                 const void* decoder_packed, const bdh_rope* rope,
+                                 float* next_out, float* rho_out, void* stream) {
+  ProfScope prof;
+  if (!plan) return fail(BDH_EINVAL, "null plan");
+  bdh_recurrent_plan p{plan->batch, plan->heads, 1, plan->time, plan->latent, plan->embd};
+  bdh_status st = check_plan(&p);
+  if (st != BDH_OK) return st;
+  if (!current || !encoder_packed || !encoder_v_packed || !decoder_packed || !next_out)
+    return fail(BDH_EINVAL, "null tensor pointer");
+  if ((const float*)next_out == current) return fail(BDH_EINVAL, "next_out must not alias current");
+  const char* why = nullptr;
+  if (!layer_shape_supported(p.latent, p.embd, &why)) return fail(BDH_UNSUPPORTED, why);
+  if (rope && (rope->mode != BDH_ROPE_SEQUENTIAL && rope->mode != BDH_ROPE_FIXED))
+    return fail(BDH_EINVAL, "unknown rope mode");
+  if (rope && !(rope->theta > 0.0f)) return fail(BDH_EINVAL, "rope theta must be > 0");
+  if (rope && (rope->pos0 < 0 || rope->pos0 + p.time > (int64_t)1 << 24))
+    return fail(BDH_UNSUPPORTED, "positions must lie in [0, 2^24) to be exact in f32");
+  if ((p.batch * p.time + 255) / 256 * (p.heads * p.latent / 128) > ((int64_t)1 << 31) - 1)
+    return fail(BDH_UNSUPPORTED, "layer too large for one launch");
+  const float* freqs = nullptr;
+  if (rope) {
+    st = rope_freqs_device(p.latent, rope->theta, &freqs);
+    if (st != BDH_OK) return st;
+  }
+  LayerArgs a;
+  a.cur = current;
+  a.enc = (const bf16_t*)encoder_packed;
+  a.encv = (const bf16_t*)encoder_v_packed;
+  a.dec = (const bf16_t*)decoder_packed;
+  a.freqs = freqs;
+  a.pos0 = rope ? rope->pos0 : 0;
+  a.fixed = rope ? rope->mode == BDH_ROPE_FIXED : 0;
+  a.next = next_out;
+  a.rho_out = rho_out;
+  a.B = p.batch;
+  a.H = p.heads;
+  a.T = p.time;
+  a.N = p.latent;
+  a.D = p.embd;
+  a.state_interval = default_interval(p.time);
+  st = run_layer(a, (hipStream_t)stream, &prof.launches);
+  if (st == BDH_OK) prof.done(true);
+  return st;
+}
+
 void bdh_profile_enable(int32_t enabled) { g_prof_on = enabled != 0; }
 
 void bdh_profile_reset(void) {

@@ -31,6 +31,11 @@ enum ScratchSlot {
   SLOT_READOUT,      // readout partials (bf16 path) [rd_kr, S, Lp, D] f32
   SLOT_RHO_A,        // states between intervals (bf16 path) [S, N, D] f32
   SLOT_RHO_B,
+  SLOT_LAYER_CUR,    // layer input as bf16          [B, T, D]
+  SLOT_LAYER_XY,     // x, then y over it (bf16)     [B, H, T, N]
+  SLOT_LAYER_ATTN,   // attention output (f32)       [B, H, T, D]
+  SLOT_LAYER_AN,     // its LayerNorm (bf16)         [B, H, T, D]
+  SLOT_LAYER_Z,      // decoder split-K partials     [ks, B*T, D] f32
   SLOT_COUNT
 };
 bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);
@@ -76,6 +81,26 @@ struct Bf16Args {
 };
 bool bf16_shape_supported(int64_t N, int64_t D, const char** why);
 bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches);
+
+// --- low-rank layer body (layer_bf16.hip) ------------------------------------
+struct LayerArgs {
+  const float* cur;     // [B, T, D]
+  const bf16_t* enc;    // packed encoder   [H, N, D]
+  const bf16_t* encv;   // packed encoder_v [H, N, D]
+  const bf16_t* dec;    // packed decoder   [D, H*N]
+  const float* freqs;   // device RoPE frequencies or null
+  int64_t pos0;
+  int fixed;
+  float* next;          // [B, T, D]
+  float* rho_out;       // [B, H, N, D] or null (then context-only attention)
+  int64_t B, H, T, N, D;
+  int64_t state_interval;  // state-carry interval when rho_out is set
+};
+bool layer_shape_supported(int64_t N, int64_t D, const char** why);
+bdh_status pack_lowrank_weights(int64_t H, int64_t N, int64_t D, const float* enc,
+                                const float* encv, const float* dec, bf16_t* enc_p,
+                                bf16_t* encv_p, bf16_t* dec_p, hipStream_t st);
+bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches);
 
 // --- decode (decode.hip) ------------------------------------------------------
 struct DecodeArgs {

@@ -1,0 +1,109 @@
+// bf16 MFMA tile machinery shared by the prefill units (mfma_prefill.hip)
+// and the layer GEMMs (layer_bf16.hip): 256-thread workgroups whose 4 waves
+// each own a 64x128 block of v_mfma_f32_16x16x32_bf16 accumulators, operands
+// staged through LDS in 32-deep k steps (double-buffered), and an epilogue
+// that writes the accumulators back as rows through LDS.
+#pragma once
+
+#include "bdh_bf16.h"
+
+namespace bdh {
+namespace mfma {
+
+constexpr int NT = 256;               // 4 waves
+constexpr int BK = 32;                // k step: 64-byte LDS rows of four 16-byte chunks
+constexpr int ROWS = T256 + T256 / 2; // operand rows per step (256 + 128)
+constexpr int BUF = ROWS * BK;        // bf16 elements of one step's operands
+
+// Element offset of 16-byte chunk c (0..3) of LDS row r.  Chunks are XOR
+// swizzled with bits 1..2 of the row: measured on gfx950 (LDS bank-conflict
+// counter), this makes both the MFMA fragment reads (16 rows x 4 chunks per
+// wave) and the row-segment writes (4 lanes per row) conflict-free, where a
+// padded 80-byte pitch has 2x conflicts on each.
+__device__ __forceinline__ int lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 3)) << 3); }
+
+__device__ __forceinline__ bf16x8 frag(const bf16_t* base, int row, int lane) {
+  return *reinterpret_cast<const bf16x8*>(&base[lds_off(row + (lane & 15), lane >> 4)]);
+}
+
+// acc[mi][ni] += A[arow + 16 mi] x B[brow + 16 ni]^T over one 32-deep step
+// (rows of both operands k-contiguous): 4 x 8 MFMAs.  All 12 fragments are
+// requested up front, in the order the MFMAs consume them, so the first
+// MFMAs wait only for the first reads and one LDS round trip covers the step.
+__device__ __forceinline__ void mma_64x128(const bf16_t* A, const bf16_t* B, int lane, int arow,
+                                           int brow, floatx4 (&acc)[4][8]) {
+  bf16x8 af[4], bfr[8];
+  af[0] = frag(A, arow, lane);
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) bfr[ni] = frag(B, brow + ni * 16, lane);
+#pragma unroll
+  for (int mi = 1; mi < 4; ++mi) af[mi] = frag(A, arow + mi * 16, lane);
+#pragma unroll
+  for (int ni = 4; ni < 8; ++ni) bfr[ni] = frag(B, brow + ni * 16, lane);
+#pragma unroll
+  for (int nh = 0; nh < 2; ++nh)
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+        acc[mi][nh * 4 + ni] = mfma16(af[mi], bfr[nh * 4 + ni], acc[mi][nh * 4 + ni]);
+}
+
+__device__ __forceinline__ void zero_acc(floatx4 (&acc)[4][8]) {
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = zero4();
+}
+
+// Epilogue of a wave's 64 x 128 fp32 accumulator block, through LDS (free
+// once the step loop's last barrier has passed): per 16-row slice mi the
+// wave writes its block to its own region (row pitch 132 floats, so the four
+// 4-row groups of one store land in distinct banks) and reads it back as
+// rows, two per instruction, 16 bytes per lane; emit(row, col, v) receives
+// row 0..63 and column 0..124 (a multiple of 4) of the block.  Every wave
+// of the workgroup must call it (it holds barriers).
+template <class Emit>
+__device__ __forceinline__ void epilogue_64x128(const floatx4 (&acc)[4][8], bf16_t* lds, int w,
+                                                int lane, Emit&& emit) {
+  constexpr int EP = 132;
+  float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) E[acc16_row(lane, r) * EP + ni * 16 + acc16_col(lane)] = acc[mi][ni][r];
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 16; rr += 2) {
+      const int row = rr + (lane >> 5), col = 4 * (lane & 31);
+      emit(mi * 16 + row, col, *reinterpret_cast<const float4*>(&E[row * EP + col]));
+    }
+    __syncthreads();
+  }
+}
+
+// Steps [kb, ke), an even count: LDS buffer (kt - kb) & 1 holds step kt; the
+// loads of step kt+1 are issued before step kt's MFMAs and written to the
+// other buffer after them.
+template <class Load, class Store, class Compute>
+__device__ __forceinline__ void run_steps(int kb, int ke, Load&& load, Store&& store,
+                                          Compute&& compute) {
+  load(kb);
+  store(0);
+  __syncthreads();
+  for (int kt = kb; kt < ke; kt += 2) {
+    load(kt + 1);
+    compute(0);
+    store(1);
+    __syncthreads();
+    if (kt + 2 < ke) load(kt + 2);
+    compute(1);
+    if (kt + 2 < ke) store(0);
+    __syncthreads();
+  }
+}
+
+}  // namespace mfma
+}  // namespace bdh

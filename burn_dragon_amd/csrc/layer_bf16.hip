@@ -1,0 +1,366 @@
+// BDH low-rank layer body around the recurrent attention, bf16 MFMA with
+// fp32 accumulation (residual_stream.rs:323-572, vanilla options: no ReLU
+// threshold, no sparse latent mask, dropout off at inference):
+//
+//   x    = ReLU(cur E_h)                 [B, H, T, N]   (GEMM X)
+//   a    = LN(attn(rope(x), v = cur))    [B, H, T, D]   (prefill_bf16.hip, ln_rows)
+//   y    = ReLU(a Ev_h) * x              [B, H, T, N]   (GEMM Y, written over x)
+//   z    = y' Dec, y' = [B*T, H*N]       [B, T, D]      (GEMM Z, split-K partials)
+//   next = LN(cur + LN(z))               [B, T, D]      (residual_kernel)
+//
+// LN is DragonNorm's LayerNorm arm with gamma = 1, beta = 0, eps = 1e-5 and
+// the biased variance (norm.rs:302-328).  The three GEMMs share the
+// 256 x 128 MFMA tile of the prefill units (bdh_mfma.h); their operands are
+// K-contiguous bf16 rows: cur and the LN'd attention rows (K = D), the
+// packed weights (encoders [H, N, D], decoder [D, H*N]) and y (K = H*N,
+// contiguous inside a head's N).
+#include "bdh_mfma.h"
+
+namespace bdh {
+namespace {
+
+using namespace mfma;
+
+enum { G_X = 0, G_Y = 1, G_Z = 2 };
+
+struct LayerGemmArgs {
+  const bf16_t* a;    // X: cur [M, D]; Y: LN'd attention [B, H, T, D]; Z: y [B, H, T, N]
+  const bf16_t* b;    // X: encoder [H*N, D]; Y: encoder_v [H*N, D]; Z: decoder [D, H*N]
+  bf16_t* xy;         // X: x out; Y: x in, y out (same place); [B, H, T, N]
+  float* zpart;       // Z: partials [ks, M, D]
+  int64_t B, H, T, N, D, M;  // M = B * T
+  int mt, ct, ks;     // tiles along M and along the output columns; Z: K splits
+};
+
+// Workgroup id -> (row tile, column tile, K split): row tiles fastest, so
+// the row tiles that share a column tile's B rows run side by side.
+template <int KIND>
+__global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * BUF];
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  int id = blockIdx.x;
+  const int mtile = id % g.mt;
+  id /= g.mt;
+  const int ctile = id % g.ct;
+  const int kp = id / g.ct;
+  const int64_t m0 = (int64_t)mtile * T256, c0 = (int64_t)ctile * (T256 / 2);
+  const int64_t K = KIND == G_Z ? g.H * g.N : g.D;
+  const int nk = (int)(K / BK);
+  const int kb = KIND == G_Z ? (int)((int64_t)nk * kp / g.ks) : 0;
+  const int ke = KIND == G_Z ? (int)((int64_t)nk * (kp + 1) / g.ks) : nk;
+  const int64_t h = KIND == G_Z ? 0 : c0 / g.N;  // head of the column tile (X, Y)
+  const int64_t ncols = KIND == G_Z ? g.D : g.H * g.N;
+
+  // Loader: 4 lanes per 64-byte row segment; groups 0..3 are A rows
+  // m0 + rb + 64 g, groups 4 and 5 are B rows c0 + rb + 64 (g - 4).  Rows
+  // past M (or past D for Z's B rows) re-read the last row and are never
+  // stored.
+  const int kc = tid & 3, rb = tid >> 2;
+  const bf16_t* arow[4];
+  const bf16_t* brow[2];
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) {
+    int64_t m = m0 + rb + 64 * gi;
+    m = m < g.M ? m : g.M - 1;
+    const int64_t bb = m / g.T, t = m - bb * g.T;
+    if (KIND == G_X) arow[gi] = g.a + m * g.D;
+    else if (KIND == G_Y) arow[gi] = g.a + ((bb * g.H + h) * g.T + t) * g.D;
+    else arow[gi] = g.a + (bb * g.H * g.T + t) * g.N;
+    arow[gi] += kc * 8;
+  }
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) {
+    int64_t c = c0 + rb + 64 * gi;
+    c = c < ncols ? c : ncols - 1;
+    brow[gi] = g.b + c * K + kc * 8;
+  }
+  uint4 st[6];
+  auto load = [&](int kt) {
+    const int64_t k0 = (int64_t)kt * BK;
+    // Z: k runs over (head, neuron); a 32-deep step stays inside one head.
+    const int64_t aoff = KIND == G_Z ? (k0 / g.N) * g.T * g.N + k0 % g.N : k0;
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) st[gi] = ldg16(arow[gi] + aoff);
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) st[4 + gi] = ldg16(brow[gi] + k0);
+  };
+  auto store = [&](int buf) {
+    bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
+#pragma unroll
+    for (int gi = 0; gi < 6; ++gi) *reinterpret_cast<uint4*>(&base[lds_off(64 * gi + rb, kc)]) = st[gi];
+  };
+
+  floatx4 acc[4][8];
+  zero_acc(acc);
+  run_steps(kb, ke, load, store, [&](int buf) {
+    mma_64x128(lds + buf * BUF, lds + buf * BUF, lane, 64 * w, T256, acc);
+  });
+
+  epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
+    const int64_t m = m0 + 64 * w + row, c = c0 + col;
+    if (m >= g.M) return;
+    if (KIND == G_Z) {
+      if (c < g.D) *reinterpret_cast<float4*>(&g.zpart[((int64_t)kp * g.M + m) * g.D + c]) = v;
+      return;
+    }
+    const int64_t bb = m / g.T, t = m - bb * g.T, n = c - h * g.N;
+    bf16_t* dst = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
+    float r[4] = {fmaxf(v.x, 0.0f), fmaxf(v.y, 0.0f), fmaxf(v.z, 0.0f), fmaxf(v.w, 0.0f)};
+    if (KIND == G_Y) {
+      const uint2 xv = *reinterpret_cast<const uint2*>(dst);
+      r[0] *= bf16_lo(xv.x);
+      r[1] *= bf16_hi(xv.x);
+      r[2] *= bf16_lo(xv.y);
+      r[3] *= bf16_hi(xv.y);
+    }
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+  });
+}
+
+// Wave-wide sum (fixed butterfly order: the same result in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+constexpr int LN_MAX = 32;  // D / 64 values per lane (D <= 2048)
+
+// LayerNorm of one D-row held 64-strided across the wave's lanes, in place:
+// (v - mean) / sqrt(var + eps), biased variance, two passes.
+template <int PER>
+__device__ __forceinline__ void ln_wave(float (&v)[LN_MAX], int D) {
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) s += v[i];
+  const float mean = wave_sum(s) / (float)D;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    v[i] -= mean;
+    q += v[i] * v[i];
+  }
+  const float den = sqrtf(wave_sum(q) / (float)D + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] /= den;
+}
+
+// out_bf16[r, :] = LN(in[r, :]) for `rows` rows of D (one wave per row).
+template <int PER>
+__global__ __launch_bounds__(256) void ln_rows_kernel(const float* __restrict__ in,
+                                                      bf16_t* __restrict__ out, int64_t rows,
+                                                      int D) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  float v[LN_MAX];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] = in[r * D + lane + 64 * i];
+  ln_wave<PER>(v, D);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) out[r * D + lane + 64 * i] = (bf16_t)v[i];
+}
+
+// next[m, :] = LN(cur[m, :] + LN(z[m, :])), z = sum of the ks partials in
+// a fixed order (one wave per token row).
+template <int PER>
+__global__ __launch_bounds__(256) void residual_kernel(const float* __restrict__ zpart,
+                                                       const float* __restrict__ cur,
+                                                       float* __restrict__ next, int64_t M,
+                                                       int D, int ks) {
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (m >= M) return;
+  float v[LN_MAX];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    float s = zpart[m * D + lane + 64 * i];
+    for (int kp = 1; kp < ks; ++kp) s += zpart[((int64_t)kp * M + m) * D + lane + 64 * i];
+    v[i] = s;
+  }
+  ln_wave<PER>(v, D);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] += cur[m * D + lane + 64 * i];
+  ln_wave<PER>(v, D);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) next[m * D + lane + 64 * i] = v[i];
+}
+
+__global__ __launch_bounds__(256) void to_bf16_kernel(const float* __restrict__ in,
+                                                      bf16_t* __restrict__ out, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (i + 4 <= n) {
+    const float4 v = *reinterpret_cast<const float4*>(in + i);
+    *reinterpret_cast<uint2*>(out + i) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+  } else {
+    for (int64_t j = i; j < n; ++j) out[j] = (bf16_t)in[j];
+  }
+}
+
+// out[b, c, r] = bf16(in[b, r, c]) for [batches, rows, cols] (32 x 32 tiles).
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const float* __restrict__ in,
+                                                             bf16_t* __restrict__ out,
+                                                             int64_t rows, int64_t cols) {
+  __shared__ float tile[32][33];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    tile[k][tx] = (r < rows && c < cols) ? in[(b * rows + r) * cols + c] : 0.0f;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (c < cols && r < rows) out[(b * cols + c) * rows + r] = (bf16_t)tile[tx][k];
+  }
+}
+
+inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+template <int KIND>
+hipError_t launch_gemm(const LayerGemmArgs& g, hipStream_t st) {
+  const unsigned grid = (unsigned)((int64_t)g.mt * g.ct * (KIND == G_Z ? g.ks : 1));
+  hipLaunchKernelGGL(layer_gemm_kernel<KIND>, dim3(grid), dim3(NT), 0, st, g);
+  return hipGetLastError();
+}
+
+template <int PER>
+hipError_t launch_ln(const float* in, bf16_t* out, int64_t rows, int D, hipStream_t st) {
+  hipLaunchKernelGGL(ln_rows_kernel<PER>, dim3(cdiv(rows, 4)), dim3(256), 0, st, in, out, rows, D);
+  return hipGetLastError();
+}
+
+template <int PER>
+hipError_t launch_residual(const float* z, const float* cur, float* next, int64_t M, int D, int ks,
+                           hipStream_t st) {
+  hipLaunchKernelGGL(residual_kernel<PER>, dim3(cdiv(M, 4)), dim3(256), 0, st, z, cur, next, M, D,
+                     ks);
+  return hipGetLastError();
+}
+
+// PER = D / 64 as a compile-time count (D a multiple of 64, at most 2048).
+template <template <int> class F, class... Args>
+hipError_t dispatch_per(int D, Args... args) {
+  switch (D / 64) {
+#define BDH_PER(p) \
+  case p:          \
+    return F<p>::run(args...);
+    BDH_PER(1) BDH_PER(2) BDH_PER(3) BDH_PER(4) BDH_PER(5) BDH_PER(6) BDH_PER(7) BDH_PER(8)
+    BDH_PER(9) BDH_PER(10) BDH_PER(11) BDH_PER(12) BDH_PER(13) BDH_PER(14) BDH_PER(15)
+    BDH_PER(16) BDH_PER(17) BDH_PER(18) BDH_PER(19) BDH_PER(20) BDH_PER(21) BDH_PER(22)
+    BDH_PER(23) BDH_PER(24) BDH_PER(25) BDH_PER(26) BDH_PER(27) BDH_PER(28) BDH_PER(29)
+    BDH_PER(30) BDH_PER(31) BDH_PER(32)
+#undef BDH_PER
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+template <int PER>
+struct LnF {
+  static hipError_t run(const float* in, bf16_t* out, int64_t rows, int D, hipStream_t st) {
+    return launch_ln<PER>(in, out, rows, D, st);
+  }
+};
+template <int PER>
+struct ResF {
+  static hipError_t run(const float* z, const float* cur, float* next, int64_t M, int D, int ks,
+                        hipStream_t st) {
+    return launch_residual<PER>(z, cur, next, M, D, ks, st);
+  }
+};
+
+}  // namespace
+
+bool layer_shape_supported(int64_t N, int64_t D, const char** why) {
+  if (!bf16_shape_supported(N, D, why)) return false;
+  if (D % 64 != 0 || D > 64 * LN_MAX) {
+    if (why) *why = "layer needs embd % 64 == 0 and embd <= 2048";
+    return false;
+  }
+  return true;
+}
+
+bdh_status pack_lowrank_weights(int64_t H, int64_t N, int64_t D, const float* enc,
+                                const float* encv, const float* dec, bf16_t* enc_p,
+                                bf16_t* encv_p, bf16_t* dec_p, hipStream_t st) {
+  // encoders [H, D, N] -> [H, N, D]; decoder [H*N, D] -> [D, H*N]
+  const dim3 ge(cdiv(N, 32), cdiv(D, 32), (unsigned)H);
+  hipLaunchKernelGGL(transpose_bf16_kernel, ge, dim3(256), 0, st, enc, enc_p, D, N);
+  hipLaunchKernelGGL(transpose_bf16_kernel, ge, dim3(256), 0, st, encv, encv_p, D, N);
+  const dim3 gd(cdiv(D, 32), cdiv(H * N, 32), 1);
+  hipLaunchKernelGGL(transpose_bf16_kernel, gd, dim3(256), 0, st, dec, dec_p, H * N, D);
+  BDH_HIP_TRY(hipGetLastError());
+  return BDH_OK;
+}
+
+bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
+  const int64_t S = a.B * a.H, M = a.B * a.T, HN = a.H * a.N;
+  void *curb = nullptr, *xy = nullptr, *attn = nullptr, *an = nullptr, *zp = nullptr;
+  // Decoder split-K: the fewest splits (each an even number of 32-deep
+  // steps) that give at least two workgroups per CU.
+  const int64_t nkz = HN / 32;
+  const int64_t tiles_z = (int64_t)cdiv(M, T256) * cdiv(a.D, T256 / 2);
+  int ks = 1;
+  for (int cand = 1; cand <= 16 && nkz % (2 * cand) == 0; cand *= 2) {
+    ks = cand;
+    if (tiles_z * cand >= 512) break;
+  }
+  bdh_status s = scratch(SLOT_LAYER_CUR, (size_t)(M * a.D) * sizeof(bf16_t), &curb);
+  if (s != BDH_OK) return s;
+  s = scratch(SLOT_LAYER_XY, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xy);
+  if (s != BDH_OK) return s;
+  s = scratch(SLOT_LAYER_ATTN, (size_t)(S * a.T * a.D) * sizeof(float), &attn);
+  if (s != BDH_OK) return s;
+  s = scratch(SLOT_LAYER_AN, (size_t)(S * a.T * a.D) * sizeof(bf16_t), &an);
+  if (s != BDH_OK) return s;
+  s = scratch(SLOT_LAYER_Z, (size_t)(ks * M * a.D) * sizeof(float), &zp);
+  if (s != BDH_OK) return s;
+
+  hipLaunchKernelGGL(to_bf16_kernel, dim3(cdiv(M * a.D, 1024)), dim3(256), 0, st, a.cur,
+                     (bf16_t*)curb, M * a.D);
+  BDH_HIP_TRY(hipGetLastError());
+  LayerGemmArgs g{};
+  g.B = a.B; g.H = a.H; g.T = a.T; g.N = a.N; g.D = a.D; g.M = M;
+  g.mt = (int)cdiv(M, T256);
+  g.ct = (int)(HN / (T256 / 2));
+  g.ks = 1;
+  g.a = (const bf16_t*)curb;
+  g.b = a.enc;
+  g.xy = (bf16_t*)xy;
+  BDH_HIP_TRY(launch_gemm<G_X>(g, st));
+
+  Bf16Args b;
+  b.x = (const bf16_t*)xy;
+  b.v = (const bf16_t*)curb;
+  b.rho_in = nullptr;
+  b.decay = nullptr;
+  b.freqs = a.freqs;
+  b.pos0 = a.pos0;
+  b.fixed = a.fixed;
+  b.ctx = (float*)attn;
+  b.rho_out = a.rho_out;
+  b.B = a.B; b.H = a.H; b.Hv = 1; b.T = a.T; b.N = a.N; b.D = a.D;
+  b.state = a.rho_out != nullptr;
+  b.L = b.state ? a.state_interval : ((a.T + 127) / 128) * 128;
+  uint64_t n_attn = 0;
+  s = run_bf16_path(b, st, &n_attn);
+  if (s != BDH_OK) return s;
+
+  BDH_HIP_TRY(dispatch_per<LnF>((int)a.D, (const float*)attn, (bf16_t*)an, S * a.T, (int)a.D, st));
+  g.a = (const bf16_t*)an;
+  g.b = a.encv;
+  BDH_HIP_TRY(launch_gemm<G_Y>(g, st));
+  g.a = (const bf16_t*)xy;
+  g.b = a.dec;
+  g.ct = (int)cdiv(a.D, T256 / 2);
+  g.ks = ks;
+  g.zpart = (float*)zp;
+  BDH_HIP_TRY(launch_gemm<G_Z>(g, st));
+  BDH_HIP_TRY(dispatch_per<ResF>((int)a.D, (const float*)zp, a.cur, a.next, M, (int)a.D, ks, st));
+  if (launches) *launches += 6 + n_attn;
+  return BDH_OK;
+}
+
+}  // namespace bdh

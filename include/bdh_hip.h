@@ -127,6 +127,39 @@ bdh_status bdh_dense_causal_attention_fwd(const bdh_recurrent_plan* plan, int32_
                                           const float* decay, float* context_out,
                                           void* stream);
 
+/* Low-rank BDH layer body around the recurrent attention, bf16 MFMA with
+ * fp32 accumulation.  Replaces lowrank_residual_step_impl
+ * (crates/burn_dragon_core/src/model/residual_stream.rs:323-572) with its
+ * default options (no ReLU threshold, no sparse latent mask, dropout off):
+ *   x    = ReLU(cur E_h)                       per head h, [B,H,T,N]
+ *   a    = LN(attention(rope(x), value = cur))  (sequence_dispatch.rs:83-136)
+ *   y    = ReLU(a Ev_h) * x
+ *   next = LN(cur + LN(decode_y_neuron_tail(y, Dec)))   (:309-321)
+ * LN = DragonNorm LayerNorm with gamma = 1, beta = 0, eps = 1e-5 (norm.rs:302-328).
+ * current, next_out [B,T,D] f32 (Burn's [B,1,T,D]); weights packed by
+ * bdh_lowrank_pack_weights; rope may be NULL (no rotation); rho_out
+ * [B,H,N,D] f32, or NULL when the terminal state is not retained.
+ * Needs latent % 256 == 0 and embd % 64 == 0, embd <= 2048. */
+typedef struct {
+  int64_t batch, heads, time, latent, embd;
+} bdh_layer_plan;
+
+/* The layer's weights in the operand layouts of bdh_lowrank_layer_fwd:
+ * encoder, encoder_v [H,D,N] f32 (Burn [1,H,D,N]) -> [H,N,D] bf16;
+ * decoder [H*N, D] f32 -> [D, H*N] bf16.  Outputs are caller-owned device
+ * buffers of H*N*D bf16 elements each.  Pack once per weight set (the
+ * reference shares the weights across layers, dragon.rs:3358). */
+bdh_status bdh_lowrank_pack_weights(int64_t heads, int64_t latent, int64_t embd,
+                                    const float* encoder, const float* encoder_v,
+                                    const float* decoder, void* encoder_packed,
+                                    void* encoder_v_packed, void* decoder_packed,
+                                    void* stream);
+
+bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* current,
+                                 const void* encoder_packed, const void* encoder_v_packed,
+                                 const void* decoder_packed, const bdh_rope* rope,
+                                 float* next_out, float* rho_out, void* stream);
+
 /* Profiling counters with the field names of KernelProfileSnapshot
  * (crates/burn_dragon_kernel/src/profiling.rs:3-16).  Host wall-clock
  * nanoseconds of the entry points; collected only while enabled (the

@@ -188,6 +188,52 @@ def ndarray_recurrent_f32(q, v, rho0=None, decay=None, threads: int = 0):
     return ctx, rho, secs
 
 
+def layer_norm_f64(x, eps: float = 1e-5) -> np.ndarray:
+    """DragonNorm::forward, LayerNorm arm with gamma = 1, beta = 0
+    (crates/burn_dragon_core/src/model/norm.rs:302-328): (x - mean) /
+    sqrt(var + eps) over the last axis, var the biased variance
+    (var_mean_bias).  f64."""
+    x = np.asarray(x, np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    return (x - mean) / np.sqrt(var + eps)
+
+
+def decode_y_neuron_tail_f64(y, decoder) -> np.ndarray:
+    """decode_y_neuron_tail (residual_stream.rs:309-321): y [B,H,T,N] ->
+    swap_dims(1, 2) -> [B*T, H*N] @ decoder [H*N, D] -> [B,T,D]."""
+    y = np.asarray(y, np.float64)
+    B, H, T, N = y.shape
+    dec = np.asarray(decoder, np.float64)
+    return (y.transpose(0, 2, 1, 3).reshape(B * T, H * N) @ dec).reshape(B, T, dec.shape[1])
+
+
+def lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=0, theta: float = 65536.0,
+                      rho0=None):
+    """lowrank_residual_step_impl (residual_stream.rs:323-572) with its
+    default options (no ReLU threshold, no sparse latent mask, dropout off):
+      x = ReLU(cur @ E_h)                                  (:377-395)
+      attn = recurrent attention of rope(x) with value cur  (:398;
+             sequence_dispatch.rs:97-111; linear.rs:18-60)
+      attn = LN(attn)                                      (:422)
+      y = x * ReLU(attn @ Ev_h)                            (:440-486)
+      mlp = LN(decode_y_neuron_tail(y, Dec))               (:488, :499)
+      next = LN(cur + mlp)                                 (:517)
+    cur [B,T,D]; encoder, encoder_v [H,D,N]; decoder [H*N,D]; pos0 None = no
+    RoPE.  RoPE runs in the reference's f32 op order, everything else in f64.
+    Returns (next [B,T,D], rho [B,H,N,D])."""
+    cur = np.asarray(cur, np.float64)
+    enc = np.asarray(encoder, np.float64)
+    encv = np.asarray(encoder_v, np.float64)
+    x = np.maximum(np.einsum("btd,hdn->bhtn", cur, enc), 0.0)
+    q = rope_rotate(x.astype(np.float32), pos0=pos0, theta=theta) if pos0 is not None else x
+    ctx, rho = recurrent_f64(q, cur[:, None].astype(np.float32), rho0)
+    a = layer_norm_f64(ctx)
+    y = x * np.maximum(np.einsum("bhtd,hdn->bhtn", a, encv), 0.0)
+    mlp = layer_norm_f64(decode_y_neuron_tail_f64(y, decoder))
+    return layer_norm_f64(cur + mlp), rho
+
+
 def rel_l2(a, b) -> float:
     """||a - b||_2 / ||b||_2 in f64 (b is the reference)."""
     a = np.asarray(a, np.float64)

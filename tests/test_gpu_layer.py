@@ -1,0 +1,76 @@
+"""Low-rank layer body (bdh_lowrank_layer_fwd) vs the CPU oracle
+(oracle.lowrank_layer_f64, pinned in tests/test_oracle_layer.py): rel-L2 <=
+1e-2 on next and on rho, bf16 MFMA with fp32 accumulation.  The oracle gets
+the bf16-rounded weights the packed layout holds and the f32 layer input."""
+import numpy as np
+import pytest
+
+from tests.gpu_util import TOL_BF16, announce, dev, host, need_gpu, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(rng, B, H, T, N, D):
+    cur = rng.standard_normal((B, T, D)).astype(np.float32)
+    enc = (rng.standard_normal((H, D, N)) * 0.02 * 8 / np.sqrt(D / 64)).astype(np.float32)
+    encv = (rng.standard_normal((H, D, N)) * 0.02 * 8 / np.sqrt(D / 64)).astype(np.float32)
+    dec = (rng.standard_normal((H * N, D)) * 0.02).astype(np.float32)
+    return cur, enc, encv, dec
+
+
+@pytest.mark.parametrize("B,H,T,N,D,pos,want_rho", [
+    (2, 2, 200, 256, 64, 5, False),     # ragged rows (M = 400), context-only attention
+    (1, 4, 300, 512, 128, 0, True),     # rho out: one 300-token state interval
+    (1, 2, 640, 256, 256, 17, True),    # two state intervals (512 + 128), D = 256
+])
+def test_layer_matches_oracle(oracle, B, H, T, N, D, pos, want_rho):
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(B * 1000 + T + N + D)
+    cur, enc, encv, dec = _case(rng, B, H, T, N, D)
+    w = bd.LowRankWeights.pack(dev(torch, enc[None]), dev(torch, encv[None]), dev(torch, dec))
+    assert w is not None
+    announce("layer", B, H, T, N, D, pos, want_rho)
+    out = bd.lowrank_layer_forward(dev(torch, cur), w, position=pos, want_rho=want_rho)
+    torch.cuda.synchronize()
+    assert out is not None
+    nref, rref = oracle.lowrank_layer_f64(cur, oracle.round_bf16(enc), oracle.round_bf16(encv),
+                                          oracle.round_bf16(dec), pos0=pos)
+    e_next = rel_l2(host(out.next), nref)
+    msg = f"rel-L2 next {e_next:.2e}"
+    if want_rho:
+        e_rho = rel_l2(host(out.rho), rref)
+        msg += f" rho {e_rho:.2e}"
+        assert e_rho <= TOL_BF16, msg
+    print(msg)
+    assert e_next <= TOL_BF16, msg
+
+
+def test_layer_pack_is_a_transpose(oracle):
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(2)
+    H, D, N = 2, 64, 256
+    enc = rng.standard_normal((H, D, N)).astype(np.float32)
+    encv = rng.standard_normal((H, D, N)).astype(np.float32)
+    dec = rng.standard_normal((H * N, D)).astype(np.float32)
+    announce("layer pack")
+    w = bd.LowRankWeights.pack(dev(torch, enc), dev(torch, encv), dev(torch, dec))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(w.encoder), oracle.round_bf16(enc.transpose(0, 2, 1)))
+    assert np.array_equal(host(w.encoder_v), oracle.round_bf16(encv.transpose(0, 2, 1)))
+    assert np.array_equal(host(w.decoder), oracle.round_bf16(dec.T))
+
+
+def test_layer_unsupported_shapes_return_none():
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(3)
+    # embd not a multiple of 64 -> None (the caller keeps its Burn-op path)
+    cur, enc, encv, dec = _case(rng, 1, 2, 64, 256, 96)
+    w = bd.LowRankWeights.pack(dev(torch, enc), dev(torch, encv), dev(torch, dec))
+    announce("layer unsupported")
+    assert bd.lowrank_layer_forward(dev(torch, cur), w) is None
+    # embd mismatch between input and weights -> None
+    cur2 = rng.standard_normal((1, 64, 64)).astype(np.float32)
+    assert bd.lowrank_layer_forward(dev(torch, cur2), w) is None
