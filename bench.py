@@ -51,7 +51,9 @@ def parse():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--decode-warmup", type=int, default=4)
     ap.add_argument("--decode-prefill", type=int, default=1024, help="tokens prefilled into rho")
-    ap.add_argument("--only", choices=("all", "prefill", "decode", "long", "copy"), default="all",
+    ap.add_argument("--model-steps", type=int, default=2, help="timed C5 model forwards")
+    ap.add_argument("--only", choices=("all", "prefill", "decode", "long", "model", "copy"),
+                    default="all",
                     help="one leg only; 'copy' times a 1 GiB device copy (the calibration kernel "
                          "of the FETCH_SIZE / WRITE_SIZE counter runs)")
     ap.add_argument("--long-steps", type=int, default=3, help="timed C4 prefills")
@@ -306,6 +308,52 @@ def cpu_baseline_decode(target_s: float):
                       f"op-sequence step over all N*D of rho, {t_total:.2f} s wall"}
 
 
+def bench_model(torch, args):
+    """6-layer BDH forward over a byte vocabulary, B16 T1024
+    D256 nh4 N8192, low-rank weights shared across layers (std 0.02 random
+    init), uniform random tokens: embed + LN, 6 x layer body (bf16 MFMA
+    GEMMs, RoPE-fused attention), logits."""
+    import burn_dragon_amd as bd
+    B, T, V, D, H, N, L = 16, 1024, 256, 256, 4, 8192, 6
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(SEED + 5)
+    std = 0.02
+    w = bd.pack_model(torch.randn(V, D, generator=g, device=dev) * std,
+                      torch.randn(1, H, D, N, generator=g, device=dev) * std,
+                      torch.randn(1, H, D, N, generator=g, device=dev) * std,
+                      torch.randn(H * N, D, generator=g, device=dev) * std,
+                      torch.randn(D, V, generator=g, device=dev) * std, L)
+    if w is None:
+        raise RuntimeError("model weights unsupported")
+    tokens = torch.randint(0, V, (B, T), generator=g, device=dev, dtype=torch.int32)
+    for _ in range(1):
+        assert bd.model_forward_logits(tokens, w, position=0) is not None
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    steps = args.model_steps
+    e0.record()
+    for _ in range(steps):
+        bd.model_forward_logits(tokens, w, position=0)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    M, HN, C = B * T, H * N, 128
+    per_layer = 3 * 2 * M * D * HN + B * H * T * (4 * N * D + (C - 1) * (N + D))
+    flop = L * per_layer + 2 * M * D * V
+    achieved = flop / (ms * 1e-3) / 1e12
+    print(f"[model] {ms:.2f} ms/forward, {M / (ms * 1e-3) / 1e6:.2f} M tok/s, "
+          f"{achieved:.1f} TFLOP/s", flush=True)
+    return {"metric": "C5 6-layer BDH forward tokens/s", "value": M / (ms * 1e-3),
+            "unit": "tokens/s", "ms_per_forward": ms, "steps": steps,
+            "config": {"workload": "C5 6-layer BDH forward, byte vocabulary: B16 T1024 D256 nh4 "
+                                   "N8192, shared low-rank weights std 0.02, bf16 MFMA / fp32 acc, "
+                                   "RoPE fused, random tokens"},
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                         "traffic": None, "flop_per_launch": flop}}
+
+
 def bench_copy(torch):
     """A plain 1 GiB device-to-device copy: the known-size kernel against which
     the FETCH_SIZE / WRITE_SIZE counters are scaled (a copy reads and writes
@@ -351,6 +399,7 @@ def main():
     pre = bench_prefill(torch, args) if args.only in ("all", "prefill") else None
     dec = bench_decode(torch, args) if args.only in ("all", "decode") else None
     lng = bench_long(torch, args) if args.only in ("all", "long") else None
+    mdl = bench_model(torch, args) if args.only in ("all", "model") else None
 
     cpu_pre = cpu_dec = None
     if not args.no_cpu_baseline:
@@ -380,9 +429,11 @@ def main():
             out["decode"] = dec
         if lng is not None:
             out["long_prefill"] = lng
+        if mdl is not None:
+            out["model"] = mdl
     elif dec is None:
-        out = dict(lng, n_gpus=1, higher_is_better=True, scaling="weak", vs_baseline=None,
-                   dtype="bf16", data="synthetic")
+        out = dict(lng if lng is not None else mdl, n_gpus=1, higher_is_better=True,
+                   scaling="weak", vs_baseline=None, dtype="bf16", data="synthetic")
     else:
         out = {"metric": METRIC, "value": round(dec["value"], 1), "unit": "tokens/s", "n_gpus": 1,
                "steps": dec["steps"], "warmup": dec["warmup"],

@@ -66,6 +66,9 @@ SIGNATURES = {
     "bdh_lowrank_pack_weights": (_i32, [_i64] * 3 + [_vp] * 7),
     "bdh_lowrank_layer_fwd": (_i32, [ctypes.POINTER(BdhLayerPlan), _vp, _vp, _vp, _vp,
                                      ctypes.POINTER(BdhRope), _vp, _vp, _vp]),
+    "bdh_embed_norm": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
+    "bdh_lm_head_pack": (_i32, [_i64, _i64, _vp, _vp, _vp]),
+    "bdh_lm_logits": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "bdh_profile_enable": (None, [_i32]),
     "bdh_profile_reset": (None, []),
     "bdh_profile_get": (None, [ctypes.POINTER(BdhProfileSnapshot)]),

@@ -400,6 +400,50 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
   return st;
 }
 
+bdh_status bdh_embed_norm(const int32_t* tokens, int64_t n_tokens, const float* embed,
+                          int64_t vocab, int64_t embd, float* out, void* stream) {
+  ProfScope prof;
+  if (n_tokens <= 0 || vocab <= 0 || embd <= 0) return fail(BDH_UNSUPPORTED, "zero-sized dimension");
+  if (!tokens || !embed || !out) return fail(BDH_EINVAL, "null tensor pointer");
+  if (embd % 64 != 0 || embd > 2048) return fail(BDH_UNSUPPORTED, "embd % 64 == 0 and embd <= 2048 needed");
+  if ((n_tokens + 3) / 4 > ((int64_t)1 << 31) - 1) return fail(BDH_UNSUPPORTED, "too many tokens");
+  bdh_status st = embed_norm(tokens, n_tokens, embed, vocab, embd, out, (hipStream_t)stream);
+  if (st != BDH_OK) return st;
+  prof.launches = 1;
+  prof.done(true);
+  return BDH_OK;
+}
+
+bdh_status bdh_lm_head_pack(int64_t embd, int64_t vocab, const float* lm_head, void* packed,
+                            void* stream) {
+  ProfScope prof;
+  if (vocab <= 0 || embd <= 0) return fail(BDH_UNSUPPORTED, "zero-sized dimension");
+  if (!lm_head || !packed) return fail(BDH_EINVAL, "null tensor pointer");
+  if ((embd + 31) / 32 > kMaxGrid) return fail(BDH_UNSUPPORTED, "embd too large");
+  bdh_status st = pack_lm_head(embd, vocab, lm_head, (bf16_t*)packed, (hipStream_t)stream);
+  if (st != BDH_OK) return st;
+  prof.launches = 1;
+  prof.done(true);
+  return BDH_OK;
+}
+
+bdh_status bdh_lm_logits(const float* hidden, int64_t rows, int64_t embd,
+                         const void* lm_head_packed, int64_t vocab, float* logits,
+                         void* stream) {
+  ProfScope prof;
+  if (rows <= 0 || vocab <= 0 || embd <= 0) return fail(BDH_UNSUPPORTED, "zero-sized dimension");
+  if (!hidden || !lm_head_packed || !logits) return fail(BDH_EINVAL, "null tensor pointer");
+  if (embd % 64 != 0) return fail(BDH_UNSUPPORTED, "embd % 64 == 0 needed");
+  if ((rows + 255) / 256 * ((vocab + 127) / 128) > ((int64_t)1 << 31) - 1)
+    return fail(BDH_UNSUPPORTED, "too large for one launch");
+  bdh_status st = lm_logits(hidden, rows, embd, (const bf16_t*)lm_head_packed, vocab, logits,
+                            (hipStream_t)stream);
+  if (st != BDH_OK) return st;
+  prof.launches = 2;
+  prof.done(true);
+  return BDH_OK;
+}
+
 void bdh_profile_enable(int32_t enabled) { g_prof_on = enabled != 0; }
 
 void bdh_profile_reset(void) {

@@ -101,6 +101,11 @@ bdh_status pack_lowrank_weights(int64_t H, int64_t N, int64_t D, const float* en
                                 const float* encv, const float* dec, bf16_t* enc_p,
                                 bf16_t* encv_p, bf16_t* dec_p, hipStream_t st);
 bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches);
+bdh_status embed_norm(const int32_t* tokens, int64_t n, const float* embed, int64_t vocab,
+                      int64_t D, float* out, hipStream_t st);
+bdh_status pack_lm_head(int64_t D, int64_t V, const float* head, bf16_t* packed, hipStream_t st);
+bdh_status lm_logits(const float* hidden, int64_t M, int64_t D, const bf16_t* head, int64_t V,
+                     float* logits, hipStream_t st);
 
 // --- decode (decode.hip) ------------------------------------------------------
 struct DecodeArgs {

@@ -21,14 +21,16 @@ namespace {
 
 using namespace mfma;
 
-enum { G_X = 0, G_Y = 1, G_Z = 2 };
+enum { G_X = 0, G_Y = 1, G_Z = 2, G_L = 3 };
 
 struct LayerGemmArgs {
-  const bf16_t* a;    // X: cur [M, D]; Y: LN'd attention [B, H, T, D]; Z: y [B, H, T, N]
-  const bf16_t* b;    // X: encoder [H*N, D]; Y: encoder_v [H*N, D]; Z: decoder [D, H*N]
+  const bf16_t* a;    // X, L: rows [M, D]; Y: LN'd attention [B, H, T, D]; Z: y [B, H, T, N]
+  const bf16_t* b;    // X: encoder [H*N, D]; Y: encoder_v [H*N, D]; Z: decoder [D, H*N];
+                      // L: lm_head [V, D]
   bf16_t* xy;         // X: x out; Y: x in, y out (same place); [B, H, T, N]
-  float* zpart;       // Z: partials [ks, M, D]
+  float* zpart;       // Z: partials [ks, M, D]; L: logits [M, V]
   int64_t B, H, T, N, D, M;  // M = B * T
+  int64_t V;          // L: vocabulary
   int mt, ct, ks;     // tiles along M and along the output columns; Z: K splits
 };
 
@@ -48,8 +50,8 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
   const int nk = (int)(K / BK);
   const int kb = KIND == G_Z ? (int)((int64_t)nk * kp / g.ks) : 0;
   const int ke = KIND == G_Z ? (int)((int64_t)nk * (kp + 1) / g.ks) : nk;
-  const int64_t h = KIND == G_Z ? 0 : c0 / g.N;  // head of the column tile (X, Y)
-  const int64_t ncols = KIND == G_Z ? g.D : g.H * g.N;
+  const int64_t h = (KIND == G_X || KIND == G_Y) ? c0 / g.N : 0;  // head of the column tile
+  const int64_t ncols = KIND == G_Z ? g.D : KIND == G_L ? g.V : g.H * g.N;
 
   // Loader: 4 lanes per 64-byte row segment; groups 0..3 are A rows
   // m0 + rb + 64 g, groups 4 and 5 are B rows c0 + rb + 64 (g - 4).  Rows
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
     int64_t m = m0 + rb + 64 * gi;
     m = m < g.M ? m : g.M - 1;
     const int64_t bb = m / g.T, t = m - bb * g.T;
-    if (KIND == G_X) arow[gi] = g.a + m * g.D;
+    if (KIND == G_X || KIND == G_L) arow[gi] = g.a + m * g.D;
     else if (KIND == G_Y) arow[gi] = g.a + ((bb * g.H + h) * g.T + t) * g.D;
     else arow[gi] = g.a + (bb * g.H * g.T + t) * g.N;
     arow[gi] += kc * 8;
@@ -96,6 +98,46 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
     mma_64x128(lds + buf * BUF, lds + buf * BUF, lane, 64 * w, T256, acc);
   });
 
+  if (KIND == G_Y) {
+    // As epilogue_64x128, with the 8 x reads of a 16-row slice issued
+    // before any y store: y overwrites x in place, so the compiler could not
+    // move one row's load above another row's store, and each read would be
+    // a round trip of its own.
+    constexpr int EP = 132;
+    float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
+    const int col = 4 * (lane & 31);
+    const int64_t c = c0 + col, n = c - h * g.N;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+      for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) E[acc16_row(lane, r) * EP + ni * 16 + acc16_col(lane)] = acc[mi][ni][r];
+      __syncthreads();
+      bf16_t* dst[8];
+      uint2 xv[8];
+#pragma unroll
+      for (int rr = 0; rr < 8; ++rr) {
+        int64_t m = m0 + 64 * w + mi * 16 + 2 * rr + (lane >> 5);
+        m = m < g.M ? m : g.M - 1;  // rows past M re-read the last row, never stored
+        const int64_t bb = m / g.T, t = m - bb * g.T;
+        dst[rr] = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
+        xv[rr] = *reinterpret_cast<const uint2*>(dst[rr]);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 8; ++rr) {
+        const int row = 2 * rr + (lane >> 5);
+        const float4 v = *reinterpret_cast<const float4*>(&E[row * EP + col]);
+        const float y0 = fmaxf(v.x, 0.0f) * bf16_lo(xv[rr].x), y1 = fmaxf(v.y, 0.0f) * bf16_hi(xv[rr].x);
+        const float y2 = fmaxf(v.z, 0.0f) * bf16_lo(xv[rr].y), y3 = fmaxf(v.w, 0.0f) * bf16_hi(xv[rr].y);
+        if (m0 + 64 * w + mi * 16 + row < g.M)
+          *reinterpret_cast<uint2*>(dst[rr]) = make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
+      }
+      __syncthreads();
+    }
+    return;
+  }
+
   epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
     const int64_t m = m0 + 64 * w + row, c = c0 + col;
     if (m >= g.M) return;
@@ -103,16 +145,21 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
       if (c < g.D) *reinterpret_cast<float4*>(&g.zpart[((int64_t)kp * g.M + m) * g.D + c]) = v;
       return;
     }
+    if (KIND == G_L) {
+      float* dst = g.zpart + m * g.V + c;
+      if (c + 3 < g.V && (g.V & 3) == 0) {
+        *reinterpret_cast<float4*>(dst) = v;
+      } else {
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (c + j < g.V) dst[j] = e[j];
+      }
+      return;
+    }
     const int64_t bb = m / g.T, t = m - bb * g.T, n = c - h * g.N;
     bf16_t* dst = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
-    float r[4] = {fmaxf(v.x, 0.0f), fmaxf(v.y, 0.0f), fmaxf(v.z, 0.0f), fmaxf(v.w, 0.0f)};
-    if (KIND == G_Y) {
-      const uint2 xv = *reinterpret_cast<const uint2*>(dst);
-      r[0] *= bf16_lo(xv.x);
-      r[1] *= bf16_hi(xv.x);
-      r[2] *= bf16_lo(xv.y);
-      r[3] *= bf16_hi(xv.y);
-    }
+    const float r[4] = {fmaxf(v.x, 0.0f), fmaxf(v.y, 0.0f), fmaxf(v.z, 0.0f), fmaxf(v.w, 0.0f)};
     *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
   });
 }
@@ -184,6 +231,26 @@ __global__ __launch_bounds__(256) void residual_kernel(const float* __restrict__
   ln_wave<PER>(v, D);
 #pragma unroll
   for (int i = 0; i < PER; ++i) next[m * D + lane + 64 * i] = v[i];
+}
+
+// out[i, :] = LN(embed[tokens[i], :]) (one wave per token); ids outside
+// [0, vocab) give a zero row (LN of zeros is zeros).
+template <int PER>
+__global__ __launch_bounds__(256) void embed_norm_kernel(const int32_t* __restrict__ tokens,
+                                                         const float* __restrict__ embed,
+                                                         float* __restrict__ out, int64_t n,
+                                                         int64_t vocab, int D) {
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= n) return;
+  const int32_t id = tokens[i];
+  const bool ok = id >= 0 && (int64_t)id < vocab;
+  float v[LN_MAX];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) v[k] = ok ? embed[(int64_t)id * D + lane + 64 * k] : 0.0f;
+  ln_wave<PER>(v, D);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) out[i * D + lane + 64 * k] = v[k];
 }
 
 __global__ __launch_bounds__(256) void to_bf16_kernel(const float* __restrict__ in,
@@ -264,6 +331,15 @@ struct LnF {
   }
 };
 template <int PER>
+struct EmbF {
+  static hipError_t run(const int32_t* tokens, const float* embed, float* out, int64_t n,
+                        int64_t vocab, int D, hipStream_t st) {
+    hipLaunchKernelGGL(embed_norm_kernel<PER>, dim3(cdiv(n, 4)), dim3(256), 0, st, tokens, embed,
+                       out, n, vocab, D);
+    return hipGetLastError();
+  }
+};
+template <int PER>
 struct ResF {
   static hipError_t run(const float* z, const float* cur, float* next, int64_t M, int D, int ks,
                         hipStream_t st) {
@@ -292,6 +368,40 @@ bdh_status pack_lowrank_weights(int64_t H, int64_t N, int64_t D, const float* en
   const dim3 gd(cdiv(D, 32), cdiv(H * N, 32), 1);
   hipLaunchKernelGGL(transpose_bf16_kernel, gd, dim3(256), 0, st, dec, dec_p, H * N, D);
   BDH_HIP_TRY(hipGetLastError());
+  return BDH_OK;
+}
+
+bdh_status embed_norm(const int32_t* tokens, int64_t n, const float* embed, int64_t vocab,
+                      int64_t D, float* out, hipStream_t st) {
+  BDH_HIP_TRY(dispatch_per<EmbF>((int)D, tokens, embed, out, n, vocab, (int)D, st));
+  return BDH_OK;
+}
+
+bdh_status pack_lm_head(int64_t D, int64_t V, const float* head, bf16_t* packed, hipStream_t st) {
+  // [D, V] -> [V, D]
+  hipLaunchKernelGGL(transpose_bf16_kernel, dim3(cdiv(V, 32), cdiv(D, 32), 1), dim3(256), 0, st,
+                     head, packed, D, V);
+  BDH_HIP_TRY(hipGetLastError());
+  return BDH_OK;
+}
+
+bdh_status lm_logits(const float* hidden, int64_t M, int64_t D, const bf16_t* head, int64_t V,
+                     float* logits, hipStream_t st) {
+  void* hb = nullptr;
+  bdh_status s = scratch(SLOT_LAYER_CUR, (size_t)(M * D) * sizeof(bf16_t), &hb);
+  if (s != BDH_OK) return s;
+  hipLaunchKernelGGL(to_bf16_kernel, dim3(cdiv(M * D, 1024)), dim3(256), 0, st, hidden,
+                     (bf16_t*)hb, M * D);
+  BDH_HIP_TRY(hipGetLastError());
+  LayerGemmArgs g{};
+  g.a = (const bf16_t*)hb;
+  g.b = head;
+  g.zpart = logits;
+  g.B = 1; g.H = 1; g.T = M; g.N = 1; g.D = D; g.M = M; g.V = V;
+  g.mt = (int)cdiv(M, T256);
+  g.ct = (int)cdiv(V, T256 / 2);
+  g.ks = 1;
+  BDH_HIP_TRY(launch_gemm<G_L>(g, st));
   return BDH_OK;
 }
 

@@ -160,6 +160,24 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
                                  const void* decoder_packed, const bdh_rope* rope,
                                  float* next_out, float* rho_out, void* stream);
 
+/* The model's input: out = LN(embed[token]) per token, the embedding lookup
+ * followed by DragonModel's input norm (dragon.rs:3352, norm.rs:302-328).
+ * tokens [n] int32, embed [vocab, embd] f32, out [n, embd] f32 (device).
+ * Ids outside [0, vocab) give a zero row.  embd % 64 == 0, embd <= 2048. */
+bdh_status bdh_embed_norm(const int32_t* tokens, int64_t n_tokens, const float* embed,
+                          int64_t vocab, int64_t embd, float* out, void* stream);
+
+/* lm_head [embd, vocab] f32 (dragon.rs:898-905) -> packed [vocab, embd] bf16
+ * for bdh_lm_logits (caller-owned, vocab*embd elements). */
+bdh_status bdh_lm_head_pack(int64_t embd, int64_t vocab, const float* lm_head, void* packed,
+                            void* stream);
+
+/* logits [rows, vocab] f32 = hidden [rows, embd] @ lm_head, bf16 MFMA with
+ * fp32 accumulation: project_hidden_to_logits (dragon.rs:4033-4055). */
+bdh_status bdh_lm_logits(const float* hidden, int64_t rows, int64_t embd,
+                         const void* lm_head_packed, int64_t vocab, float* logits,
+                         void* stream);
+
 /* Profiling counters with the field names of KernelProfileSnapshot
  * (crates/burn_dragon_kernel/src/profiling.rs:3-16).  Host wall-clock
  * nanoseconds of the entry points; collected only while enabled (the

@@ -234,6 +234,20 @@ def lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=0, theta: float = 6
     return layer_norm_f64(cur + mlp), rho
 
 
+def model_forward_f64(tokens, embed, encoder, encoder_v, decoder, lm_head, n_layer: int,
+                      pos0=0, theta: float = 65536.0) -> np.ndarray:
+    """DragonModel sequence forward with shared low-rank weights and the
+    vanilla residual connector (dragon.rs:3340-3420): current =
+    LN(embed[tokens]) (:3352), n_layer x lowrank_layer_f64 with the same
+    positions, then logits = current @ lm_head (project_hidden_to_logits,
+    :4033-4055).  tokens [B,T]; returns logits [B,T,vocab] f64."""
+    emb = np.asarray(embed, np.float64)
+    cur = layer_norm_f64(emb[np.asarray(tokens)])
+    for _ in range(n_layer):
+        cur, _ = lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=pos0, theta=theta)
+    return cur @ np.asarray(lm_head, np.float64)
+
+
 def rel_l2(a, b) -> float:
     """||a - b||_2 / ||b||_2 in f64 (b is the reference)."""
     a = np.asarray(a, np.float64)

@@ -74,3 +74,27 @@ def test_layer_unsupported_shapes_return_none():
     # embd mismatch between input and weights -> None
     cur2 = rng.standard_normal((1, 64, 64)).astype(np.float32)
     assert bd.lowrank_layer_forward(dev(torch, cur2), w) is None
+
+
+def test_model_forward_matches_oracle(oracle):
+    # embed -> LN -> 2 shared layers -> logits (vocab 256), every step on the GPU.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(77)
+    B, T, V, D, H, N, L = 2, 130, 256, 64, 2, 256, 2
+    _, enc, encv, dec = _case(rng, 1, H, 1, N, D)
+    embed = (rng.standard_normal((V, D)) * 0.02).astype(np.float32)
+    head = (rng.standard_normal((D, V)) * 0.02).astype(np.float32)
+    tokens = rng.integers(0, V, (B, T)).astype(np.int32)
+    w = bd.pack_model(dev(torch, embed), dev(torch, enc[None]), dev(torch, encv[None]),
+                      dev(torch, dec), dev(torch, head), L)
+    assert w is not None
+    announce("model forward", B, T, V, D, H, N, L)
+    logits = bd.model_forward_logits(dev(torch, tokens), w, position=0)
+    torch.cuda.synchronize()
+    assert logits is not None
+    ref = oracle.model_forward_f64(tokens, embed, oracle.round_bf16(enc), oracle.round_bf16(encv),
+                                   oracle.round_bf16(dec), oracle.round_bf16(head), L)
+    e = rel_l2(host(logits), ref)
+    print(f"rel-L2 logits {e:.2e}")
+    assert e <= TOL_BF16

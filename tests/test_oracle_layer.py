@@ -105,3 +105,23 @@ def test_layer_matches_scalar_loops_and_catches_planted_mistakes(oracle):
     for bad in ("update_before_read", "no_attn_norm", "gate_without_relu", "no_mlp_norm"):
         wrong = _layer_loops(cur, enc, encv, dec, 3, bad=bad)
         assert np.max(np.abs(got - wrong)) > 1e-3, bad
+
+
+def test_model_oracle_composition(oracle):
+    # LN(embed[tok]) -> layer -> @ lm_head, restated with the scalar loops above.
+    rng = np.random.default_rng(12)
+    V, D, H, N, T = 6, 4, 2, 4, 3
+    embed = rng.standard_normal((V, D))
+    enc = rng.standard_normal((H, D, N)) * 0.7
+    encv = rng.standard_normal((H, D, N)) * 0.7
+    dec = rng.standard_normal((H * N, D)) * 0.5
+    head = rng.standard_normal((D, V))
+    tokens = np.array([[5, 0, 3]])
+    got = oracle.model_forward_f64(tokens, embed, enc, encv, dec, head, 1, pos0=2)
+    cur = np.array([[_ln_list(list(embed[t])) for t in tokens[0]]])
+    hid = _layer_loops(cur, enc, encv, dec, 2)
+    ref = [[sum(hid[0, t, d] * head[d, v] for d in range(D)) for v in range(V)] for t in range(T)]
+    assert np.max(np.abs(got[0] - np.array(ref))) < 1e-5
+    # zero layers: logits of the normalised embeddings only
+    got0 = oracle.model_forward_f64(tokens, embed, enc, encv, dec, head, 0)
+    assert np.max(np.abs(got0[0] - cur[0] @ head)) < 1e-12
