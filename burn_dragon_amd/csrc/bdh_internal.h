@@ -33,6 +33,7 @@ enum ScratchSlot {
   SLOT_RHO_B,
   SLOT_LAYER_CUR,    // layer input as bf16          [B, T, D]
   SLOT_LAYER_XY,     // x, then y over it (bf16)     [B, H, T, N]
+  SLOT_LAYER_Q,      // rotated queries (bf16)       [B, H, T, N]
   SLOT_LAYER_ATTN,   // attention output (f32)       [B, H, T, D]
   SLOT_LAYER_AN,     // its LayerNorm (bf16)         [B, H, T, D]
   SLOT_LAYER_Z,      // decoder split-K partials     [ks, B*T, D] f32

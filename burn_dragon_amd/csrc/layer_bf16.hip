@@ -2,8 +2,9 @@
 // fp32 accumulation (residual_stream.rs:323-572, vanilla options: no ReLU
 // threshold, no sparse latent mask, dropout off at inference):
 //
-//   x    = ReLU(cur E_h)                 [B, H, T, N]   (GEMM X)
-//   a    = LN(attn(rope(x), v = cur))    [B, H, T, D]   (prefill_bf16.hip, ln_rows)
+//   x    = ReLU(cur E_h)                 [B, H, T, N]   (GEMM X, which also
+//                                                         writes q = rope(x))
+//   a    = LN(attn(q, v = cur))          [B, H, T, D]   (prefill_bf16.hip, ln_rows)
 //   y    = ReLU(a Ev_h) * x              [B, H, T, N]   (GEMM Y, written over x)
 //   z    = y' Dec, y' = [B*T, H*N]       [B, T, D]      (GEMM Z, split-K partials)
 //   next = LN(cur + LN(z))               [B, T, D]      (residual_kernel)
@@ -28,6 +29,10 @@ struct LayerGemmArgs {
   const bf16_t* b;    // X: encoder [H*N, D]; Y: encoder_v [H*N, D]; Z: decoder [D, H*N];
                       // L: lm_head [V, D]
   bf16_t* xy;         // X: x out; Y: x in, y out (same place); [B, H, T, N]
+  bf16_t* q;          // X: rope(x) out [B, H, T, N], or null (no rotation)
+  const float* freqs; // X: RoPE frequencies [N] (with q)
+  int64_t pos0;       // X: position of token 0
+  int fixed;          // X: every token at pos0
   float* zpart;       // Z: partials [ks, M, D]; L: logits [M, V]
   int64_t B, H, T, N, D, M;  // M = B * T
   int64_t V;          // L: vocabulary
@@ -158,9 +163,24 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
       return;
     }
     const int64_t bb = m / g.T, t = m - bb * g.T, n = c - h * g.N;
-    bf16_t* dst = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
+    const int64_t o = ((bb * g.H + h) * g.T + t) * g.N + n;
     const float r[4] = {fmaxf(v.x, 0.0f), fmaxf(v.y, 0.0f), fmaxf(v.z, 0.0f), fmaxf(v.w, 0.0f)};
-    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+    *reinterpret_cast<uint2*>(g.xy + o) = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+    if (g.q) {
+      // q = rope(x) from the f32 activations: pairs (n, n+1), (n+2, n+3);
+      // phase frac(p f) in the reference's f32 op order, cos / sin by
+      // v_cos_f32 / v_sin_f32 (argument in revolutions); the rotation in
+      // the op order of attention.rs:488-501.
+      const float p = (float)(g.fixed ? g.pos0 : g.pos0 + t);
+      float qv[4];
+#pragma unroll
+      for (int j = 0; j < 4; j += 2) {
+        const float fr = rope_frac(p, g.freqs[n + j]);
+        rope_pair_exact(r[j], r[j + 1], __builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr),
+                        qv[j], qv[j + 1]);
+      }
+      *reinterpret_cast<uint2*>(g.q + o) = make_uint2(pack_bf16x2(qv[0], qv[1]), pack_bf16x2(qv[2], qv[3]));
+    }
   });
 }
 
@@ -421,6 +441,11 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   if (s != BDH_OK) return s;
   s = scratch(SLOT_LAYER_XY, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xy);
   if (s != BDH_OK) return s;
+  void* q = nullptr;
+  if (a.freqs) {
+    s = scratch(SLOT_LAYER_Q, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &q);
+    if (s != BDH_OK) return s;
+  }
   s = scratch(SLOT_LAYER_ATTN, (size_t)(S * a.T * a.D) * sizeof(float), &attn);
   if (s != BDH_OK) return s;
   s = scratch(SLOT_LAYER_AN, (size_t)(S * a.T * a.D) * sizeof(bf16_t), &an);
@@ -439,16 +464,23 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   g.a = (const bf16_t*)curb;
   g.b = a.enc;
   g.xy = (bf16_t*)xy;
+  g.q = (bf16_t*)q;
+  g.freqs = a.freqs;
+  g.pos0 = a.pos0;
+  g.fixed = a.fixed;
   BDH_HIP_TRY(launch_gemm<G_X>(g, st));
+  g.q = nullptr;
 
+  // The attention reads the rotated queries GEMM X wrote (or x itself
+  // without RoPE), so it runs without a RoPE table.
   Bf16Args b;
-  b.x = (const bf16_t*)xy;
+  b.x = (const bf16_t*)(q ? q : xy);
   b.v = (const bf16_t*)curb;
   b.rho_in = nullptr;
   b.decay = nullptr;
-  b.freqs = a.freqs;
-  b.pos0 = a.pos0;
-  b.fixed = a.fixed;
+  b.freqs = nullptr;
+  b.pos0 = 0;
+  b.fixed = 0;
   b.ctx = (float*)attn;
   b.rho_out = a.rho_out;
   b.B = a.B; b.H = a.H; b.Hv = 1; b.T = a.T; b.N = a.N; b.D = a.D;
