@@ -41,6 +41,9 @@ enum ScratchSlot {
 };
 bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);
 
+// Compute units of the current device (256 on MI355X), cached per device.
+int device_cus();
+
 // Device copy of the RoPE frequency table for (latent, theta), cached.
 bdh_status rope_freqs_device(int64_t latent, float theta, const float** out);
 // Host computation of the same table (attention.rs:552-576).

@@ -39,13 +39,12 @@ struct LayerGemmArgs {
   int mt, ct, ks;     // tiles along M and along the output columns; Z: K splits
 };
 
-// Workgroup id -> (row tile, column tile, K split): row tiles fastest, so
-// the row tiles that share a column tile's B rows run side by side.
+// One output tile.  Tile id -> (row tile, column tile, K split): row tiles
+// fastest, so the row tiles that share a column tile's B rows run side by
+// side.
 template <int KIND>
-__global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
-  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * BUF];
+__device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, int id) {
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-  int id = blockIdx.x;
   const int mtile = id % g.mt;
   id /= g.mt;
   const int ctile = id % g.ct;
@@ -184,6 +183,15 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
   });
 }
 
+// Persistent: each workgroup walks tiles blockIdx.x, + gridDim.x, ...; a
+// tile's epilogue stores drain while the next tile's loads and MFMAs run.
+template <int KIND>
+__global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * BUF];
+  const int total = g.mt * g.ct * (KIND == G_Z ? g.ks : 1);
+  for (int id = blockIdx.x; id < total; id += gridDim.x) gemm_tile<KIND>(g, lds, id);
+}
+
 // Wave-wide sum (fixed butterfly order: the same result in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -308,7 +316,9 @@ inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b);
 
 template <int KIND>
 hipError_t launch_gemm(const LayerGemmArgs& g, hipStream_t st) {
-  const unsigned grid = (unsigned)((int64_t)g.mt * g.ct * (KIND == G_Z ? g.ks : 1));
+  const int64_t total = (int64_t)g.mt * g.ct * (KIND == G_Z ? g.ks : 1);
+  const int64_t slots = 2 * (int64_t)device_cus();  // two workgroups per CU
+  const unsigned grid = (unsigned)(total < slots ? total : slots);
   hipLaunchKernelGGL(layer_gemm_kernel<KIND>, dim3(grid), dim3(NT), 0, st, g);
   return hipGetLastError();
 }

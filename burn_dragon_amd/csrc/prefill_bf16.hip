@@ -264,7 +264,7 @@ bool bf16_shape_supported(int64_t N, int64_t D, const char** why) {
 }
 
 // Compute units of the current device (256 on MI355X), cached per device.
-static int device_cus() {
+int device_cus() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
