@@ -5,7 +5,8 @@
 
 namespace bdh {
 
-// Score-block (gram) and state tiles are 256 x 256.
+// Tile edge of the MFMA units: 256 rows of gram / readout tiles and of
+// v^T padding, 128 = T256 / 2 their column blocks and state neuron blocks.
 constexpr int T256 = 256;
 
 __device__ __forceinline__ uint4 ldg16(const void* p) {

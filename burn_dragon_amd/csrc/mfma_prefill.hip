@@ -1,10 +1,10 @@
-// Gram and state products of the bf16 chunked prefill (gfx950 MFMA), in one
-// launch.  Each workgroup computes a 256x128 (gram) or 128x256 (state)
-// output tile of a bf16 product with fp32 accumulation: 4 waves, each owning
-// a 64x128 block of v_mfma_f32_16x16x32_bf16 accumulators (128 AGPRs).  Two
-// workgroups share a CU (61 KB of LDS and 256 registers per lane each), so
-// while one waits on its loads, rotates its next tile or synchronises, the
-// other's MFMAs keep the matrix cores busy.
+// Gram, readout and state products of the bf16 chunked prefill (gfx950
+// MFMA), in one launch.  Each workgroup computes a 256x128 (gram, readout)
+// or 128x256 (state) output tile of a bf16 product with fp32 accumulation:
+// 4 waves, each owning a 64x128 block of v_mfma_f32_16x16x32_bf16
+// accumulators.  Two workgroups share a CU (48 KB of LDS and up to 256
+// registers per lane each), so while one waits on its loads, rotates its next
+// tile or synchronises, the other's MFMAs keep the matrix cores busy.
 //
 //   gram unit   S_kp[r, c] = sum_{n in range kp} q_r[n] q_c[n] for one
 //               256-row x 128-column tile touching an interval's lower

@@ -46,6 +46,22 @@ def test_layer_matches_oracle(oracle, B, H, T, N, D, pos, want_rho):
     assert e_next <= TOL_BF16, msg
 
 
+def test_layer_without_rope(oracle):
+    # rope = NULL: the attention sees x itself (no rotated copy is written).
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(8)
+    B, H, T, N, D = 1, 2, 256, 256, 64
+    cur, enc, encv, dec = _case(rng, B, H, T, N, D)
+    w = bd.LowRankWeights.pack(dev(torch, enc), dev(torch, encv), dev(torch, dec))
+    announce("layer no rope", B, H, T, N, D)
+    out = bd.lowrank_layer_forward(dev(torch, cur), w, position=None)
+    torch.cuda.synchronize()
+    nref, _ = oracle.lowrank_layer_f64(cur, oracle.round_bf16(enc), oracle.round_bf16(encv),
+                                       oracle.round_bf16(dec), pos0=None)
+    assert rel_l2(host(out.next), nref) <= TOL_BF16
+
+
 def test_layer_pack_is_a_transpose(oracle):
     torch = need_gpu()
     import burn_dragon_amd as bd

@@ -132,6 +132,20 @@ def test_bf16_rope_prefill_matches_oracle(oracle, B, H, Hv, T, N, D, with_rho, d
     assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
 
 
+def test_bf16_rope_fixed_mode(oracle):
+    # rotate_positions_fixed (attention.rs:512-550): every token at one position.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(41)
+    x, v, rho0 = _bf16_case(rng, 1, 2, 1, 384, 256, 64, True)
+    xb, vb = oracle.round_bf16(x), oracle.round_bf16(v)
+    announce("bf16 rope fixed", 1, 2, 384, 256, 64)
+    ctx, rho = _run(torch, bd, xb, vb, rho0, None, dtype=torch.bfloat16, rope=(1000, True))
+    q = oracle.rope_rotate(xb, pos0=1000, mode=1)
+    cref, rref = oracle.recurrent_f64(q, vb, rho0)
+    assert rel_l2(ctx, cref) <= TOL_BF16 and rel_l2(rho, rref) <= TOL_BF16
+
+
 def test_bf16_prerotated_query(oracle):
     torch = need_gpu()
     import burn_dragon_amd as bd
