@@ -164,6 +164,9 @@ bdh_status forward_common(const bdh_recurrent_plan* plan, int32_t dtype, const v
   bdh_status st = check_plan(plan);
   if (st != BDH_OK) return st;
   if (!q || !v || !ctx || (want_rho && !rho_out)) return fail(BDH_EINVAL, "null tensor pointer");
+  // The kernels move 16 bytes per lane.
+  for (const void* t : {q, v, (const void*)rho_in, (const void*)ctx, (const void*)rho_out})
+    if (((uintptr_t)t & 15) != 0) return fail(BDH_EINVAL, "tensor pointers must be 16-byte aligned");
   if (dtype != BDH_F32 && dtype != BDH_BF16) return fail(BDH_EINVAL, "unknown dtype");
   if (chunk != 0 && chunk != 128) return fail(BDH_UNSUPPORTED, "chunk must be 0 (auto) or 128");
   if (rope && (rope->mode != BDH_ROPE_SEQUENTIAL && rope->mode != BDH_ROPE_FIXED))

@@ -247,6 +247,35 @@ __global__ __launch_bounds__(256) void rope_table_bf16_kernel(const float* __res
   cs[i] = pack_bf16x2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
 }
 
+// q[s, t, :] = rope(x[s, t, :]) in bf16, 8 elements (4 pairs) per thread:
+// phase frac(p f) in the reference's f32 op order, cos / sin by v_cos_f32 /
+// v_sin_f32 of it, the rotation in f32 in the op order of
+// attention.rs:488-501, then rounded to bf16.
+__global__ __launch_bounds__(256) void rope_rotate_bf16_kernel(const bf16_t* __restrict__ x,
+                                                               const float* __restrict__ freqs,
+                                                               bf16_t* __restrict__ q, int64_t rows,
+                                                               int64_t T, int64_t N,
+                                                               int64_t pos_first, int fixed) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 8-element chunk
+  const int64_t per_row = N / 8;
+  if (i >= rows * per_row) return;
+  const int64_t row = i / per_row, n = (i - row * per_row) * 8;
+  const int64_t t = row % T;
+  const float p = (float)(fixed ? pos_first : pos_first + t);
+  const uint4 raw = *reinterpret_cast<const uint4*>(x + row * N + n);
+  const uint32_t in[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint32_t out[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float fr = rope_frac(p, freqs[n + 2 * k]);
+    float e, o;
+    rope_pair_exact(bf16_lo(in[k]), bf16_hi(in[k]), __builtin_amdgcn_cosf(fr),
+                    __builtin_amdgcn_sinf(fr), e, o);
+    out[k] = pack_bf16x2(e, o);
+  }
+  *reinterpret_cast<uint4*>(q + row * N + n) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
 }  // namespace
@@ -331,7 +360,15 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   if (stt != BDH_OK) return stt;
   stt = scratch(SLOT_SCORES, (size_t)(ks * S * n_iv * Lp * Lp) * sizeof(float), &part);
   if (stt != BDH_OK) return stt;
-  if (a.freqs) {
+  // With two or more intervals every launch would re-read the RoPE table and
+  // re-rotate its x tiles; rotating x once (one read and one write of x)
+  // lets every launch run the table-free units instead.
+  const bool prerot = a.freqs != nullptr && a.state && n_iv >= 2;
+  void* xr = nullptr;
+  if (prerot) {
+    stt = scratch(SLOT_ROTATED, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xr);
+    if (stt != BDH_OK) return stt;
+  } else if (a.freqs) {
     stt = scratch(SLOT_ROPE_TABLE, (size_t)(a.T * half) * sizeof(uint32_t), &cs);
     if (stt != BDH_OK) return stt;
   }
@@ -347,13 +384,18 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
       if (stt != BDH_OK) return stt;
     }
   }
-  const bool rope = a.freqs != nullptr;
+  const bool rope = a.freqs != nullptr && !prerot;
 
   hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, 32), cdiv(Dp, 32), (unsigned)(a.B * a.Hv)),
                      dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
   uint64_t n_launch = 1;
   BDH_HIP_TRY(hipGetLastError());
-  if (rope) {
+  if (prerot) {
+    hipLaunchKernelGGL(rope_rotate_bf16_kernel, dim3(cdiv(S * a.T * (a.N / 8), 256)), dim3(256), 0,
+                       st, a.x, a.freqs, (bf16_t*)xr, S * a.T, a.T, a.N, a.pos0, a.fixed);
+    BDH_HIP_TRY(hipGetLastError());
+    ++n_launch;
+  } else if (rope) {
     hipLaunchKernelGGL(rope_table_bf16_kernel, dim3(cdiv(a.T * half, 256)), dim3(256), 0, st,
                        a.freqs, (uint32_t*)cs, a.T, half, a.pos0, a.fixed);
     BDH_HIP_TRY(hipGetLastError());
@@ -361,7 +403,7 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   }
 
   PrefillArgs p{};
-  p.x = a.x;
+  p.x = prerot ? (const bf16_t*)xr : a.x;
   p.cs = (const uint32_t*)cs;
   p.decay = a.decay;
   p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;

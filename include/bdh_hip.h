@@ -82,7 +82,8 @@ int32_t bdh_supports_backend(void);
  * (in place); otherwise rho_in is not written (the reference's private copy,
  * recurrent.rs:259).  dtype applies to query and value: BDH_F32 runs the
  * fp32 path, BDH_BF16 the MFMA path (fp32 accumulate, fp32 rho/context).
- * chunk: causal block size for the MFMA path (0 = 128). */
+ * chunk: causal block size for the MFMA path (0 = 128).
+ * All tensor pointers must be 16-byte aligned (BDH_EINVAL otherwise). */
 bdh_status bdh_recurrent_attention_fwd(const bdh_recurrent_plan* plan, int32_t dtype,
                                        const void* query, const void* value,
                                        const float* rho_in, const float* decay,

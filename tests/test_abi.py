@@ -72,3 +72,18 @@ def test_python_surface_returns_none_without_device():
     assert bd.try_fused_recurrent_attention(q, v) is None
     assert bd.try_fused_dense_causal_attention(q, v, torch.ones(2)) is None
     assert bd.decode_step(q[:, :, 0], v[:, :, 0], torch.zeros(1, 2, 8, 8)) is None
+
+
+def test_forward_rejects_misaligned_pointers_before_any_launch():
+    # Argument checks run before any device call, so fake addresses are safe.
+    from burn_dragon_amd import _lib
+    lib = _lib.load()
+    p = _lib.BdhRecurrentPlan()
+    assert lib.bdh_recurrent_plan_new(1, 2, 1, 8, 16, 8, ctypes.byref(p)) == _lib.BDH_OK
+    good, bad = 0x10000, 0x10008
+    for q, v, ctx, rho in ((bad, good, good, good), (good, bad, good, good),
+                           (good, good, bad, good), (good, good, good, bad)):
+        st = lib.bdh_recurrent_attention_fwd(ctypes.byref(p), _lib.BDH_F32, q, v, None, None,
+                                             ctx, rho, 0, None)
+        assert st == _lib.BDH_EINVAL
+        assert "aligned" in _lib.last_error()
