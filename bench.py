@@ -52,7 +52,10 @@ def parse():
     ap.add_argument("--decode-warmup", type=int, default=4)
     ap.add_argument("--decode-prefill", type=int, default=1024, help="tokens prefilled into rho")
     ap.add_argument("--model-steps", type=int, default=2, help="timed C5 model forwards")
-    ap.add_argument("--only", choices=("all", "prefill", "decode", "long", "model", "copy"),
+    ap.add_argument("--model-decode-steps", type=int, default=32,
+                    help="timed C5 greedy decode steps")
+    ap.add_argument("--only", choices=("all", "prefill", "decode", "long", "model", "model-decode",
+                                       "copy"),
                     default="all",
                     help="one leg only; 'copy' times a 1 GiB device copy (the calibration kernel "
                          "of the FETCH_SIZE / WRITE_SIZE counter runs)")
@@ -354,6 +357,58 @@ def bench_model(torch, args):
                          "traffic": None, "flop_per_launch": flop}}
 
 
+def bench_model_decode(torch, args):
+    """Generation with the C5 model: a 1024-token prompt through the stateful
+    forward (each layer's rho kept), then greedy T = 1 steps, every layer
+    taking the sparse decode step on its own rho (generation.rs:458,
+    dragon.rs:1749-1808).  The next token is the device-side argmax of the
+    logits: no host sync inside the timed steps."""
+    import burn_dragon_amd as bd
+    B, T, V, D, H, N, L = 16, 1024, 256, 256, 4, 8192, 6
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(SEED + 6)
+    std = 0.02
+    w = bd.pack_model(torch.randn(V, D, generator=g, device=dev) * std,
+                      torch.randn(1, H, D, N, generator=g, device=dev) * std,
+                      torch.randn(1, H, D, N, generator=g, device=dev) * std,
+                      torch.randn(H * N, D, generator=g, device=dev) * std,
+                      torch.randn(D, V, generator=g, device=dev) * std, L)
+    if w is None:
+        raise RuntimeError("model weights unsupported")
+    prompt = torch.randint(0, V, (B, T), generator=g, device=dev, dtype=torch.int32)
+    state = bd.new_model_state(w, B, dev)
+    logits = bd.model_forward_logits(prompt, w, state=state)
+    if logits is None:
+        raise RuntimeError("stateful model forward failed")
+
+    def step(lg):
+        tok = lg[:, -1].argmax(-1).to(torch.int32).unsqueeze(1)
+        out = bd.model_forward_logits(tok, w, state=state)
+        if out is None:
+            raise RuntimeError("model decode step failed")
+        return out
+
+    for _ in range(args.decode_warmup):
+        logits = step(logits)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    steps = args.model_decode_steps
+    e0.record()
+    for _ in range(steps):
+        logits = step(logits)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    print(f"[model-decode] {ms:.3f} ms/token step, {B / (ms * 1e-3):.0f} tok/s "
+          f"(B{B}, {L} layers, after a {T}-token prompt)", flush=True)
+    return {"metric": "C5 6-layer BDH greedy decode tokens/s", "value": B / (ms * 1e-3),
+            "unit": "tokens/s", "ms_per_token_step": ms, "steps": steps,
+            "config": {"workload": f"C5 model decode: B{B}, {T}-token prompt, then T = 1 steps "
+                                   "with every layer's rho carried (sparse decode step), greedy "
+                                   "device-side argmax"}}
+
+
 def bench_copy(torch):
     """A plain 1 GiB device-to-device copy: the known-size kernel against which
     the FETCH_SIZE / WRITE_SIZE counters are scaled (a copy reads and writes
@@ -400,6 +455,7 @@ def main():
     dec = bench_decode(torch, args) if args.only in ("all", "decode") else None
     lng = bench_long(torch, args) if args.only in ("all", "long") else None
     mdl = bench_model(torch, args) if args.only in ("all", "model") else None
+    mdd = bench_model_decode(torch, args) if args.only in ("all", "model-decode") else None
 
     cpu_pre = cpu_dec = None
     if not args.no_cpu_baseline:
@@ -431,9 +487,12 @@ def main():
             out["long_prefill"] = lng
         if mdl is not None:
             out["model"] = mdl
+        if mdd is not None:
+            out["model_decode"] = mdd
     elif dec is None:
-        out = dict(lng if lng is not None else mdl, n_gpus=1, higher_is_better=True,
-                   scaling="weak", vs_baseline=None, dtype="bf16", data="synthetic")
+        one = next(r for r in (lng, mdl, mdd) if r is not None)
+        out = dict(one, n_gpus=1, higher_is_better=True, scaling="weak", vs_baseline=None,
+                   dtype="bf16", data="synthetic")
     else:
         out = {"metric": METRIC, "value": round(dec["value"], 1), "unit": "tokens/s", "n_gpus": 1,
                "steps": dec["steps"], "warmup": dec["warmup"],

@@ -18,4 +18,5 @@ from .attention import (CompiledDenseCausalAttentionPlan,  # noqa: F401
                         try_fused_dense_causal_attention_with_plan)
 from .decode import DecodeOutput, decode_step  # noqa: F401
 from .layer import LowRankLayerOutput, LowRankWeights, lowrank_layer_forward  # noqa: F401
-from .model import BdhModelWeights, model_forward_logits, pack_model  # noqa: F401
+from .model import (BdhModelState, BdhModelWeights, model_forward_logits, new_model_state,  # noqa: F401
+                    pack_model)

@@ -65,7 +65,7 @@ SIGNATURES = {
                                               _vp, _vp, _vp]),
     "bdh_lowrank_pack_weights": (_i32, [_i64] * 3 + [_vp] * 7),
     "bdh_lowrank_layer_fwd": (_i32, [ctypes.POINTER(BdhLayerPlan), _vp, _vp, _vp, _vp,
-                                     ctypes.POINTER(BdhRope), _vp, _vp, _vp]),
+                                     ctypes.POINTER(BdhRope), _vp, _vp, _vp, _vp]),
     "bdh_embed_norm": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
     "bdh_lm_head_pack": (_i32, [_i64, _i64, _vp, _vp, _vp]),
     "bdh_lm_logits": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),

@@ -359,7 +359,8 @@ bdh_status bdh_lowrank_pack_weights(int64_t heads, int64_t latent, int64_t embd,
 bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* current,
                                  const void* encoder_packed, const void* encoder_v_packed,
                                  const void* decoder_packed, const bdh_rope* rope,
-                                 float* next_out, float* rho_out, void* stream) {
+                                 const float* rho_in, float* next_out, float* rho_out,
+                                 void* stream) {
   ProfScope prof;
   if (!plan) return fail(BDH_EINVAL, "null plan");
   bdh_recurrent_plan p{plan->batch, plan->heads, 1, plan->time, plan->latent, plan->embd};
@@ -368,6 +369,9 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
   if (!current || !encoder_packed || !encoder_v_packed || !decoder_packed || !next_out)
     return fail(BDH_EINVAL, "null tensor pointer");
   if ((const float*)next_out == current) return fail(BDH_EINVAL, "next_out must not alias current");
+  for (const void* t : {(const void*)current, encoder_packed, encoder_v_packed, decoder_packed,
+                        (const void*)rho_in, (const void*)next_out, (const void*)rho_out})
+    if (((uintptr_t)t & 15) != 0) return fail(BDH_EINVAL, "tensor pointers must be 16-byte aligned");
   const char* why = nullptr;
   if (!layer_shape_supported(p.latent, p.embd, &why)) return fail(BDH_UNSUPPORTED, why);
   if (rope && (rope->mode != BDH_ROPE_SEQUENTIAL && rope->mode != BDH_ROPE_FIXED))
@@ -391,6 +395,7 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
   a.pos0 = rope ? rope->pos0 : 0;
   a.fixed = rope ? rope->mode == BDH_ROPE_FIXED : 0;
   a.next = next_out;
+  a.rho_in = rho_in;
   a.rho_out = rho_out;
   a.B = p.batch;
   a.H = p.heads;

@@ -37,6 +37,10 @@ enum ScratchSlot {
   SLOT_LAYER_ATTN,   // attention output (f32)       [B, H, T, D]
   SLOT_LAYER_AN,     // its LayerNorm (bf16)         [B, H, T, D]
   SLOT_LAYER_Z,      // decoder split-K partials     [ks, B*T, D] f32
+  SLOT_LAYER_RHO,    // a successor state not kept   [B, H, N, D] f32
+  SLOT_DECODE_PART,  // decode range readouts        [S, G, D] f32
+  SLOT_DECODE_IDX,   // decode range active lists    [S, N] int32
+  SLOT_DECODE_CNT,   // decode range active counts   [S, G] int32
   SLOT_COUNT
 };
 bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);
@@ -96,7 +100,8 @@ struct LayerArgs {
   int64_t pos0;
   int fixed;
   float* next;          // [B, T, D]
-  float* rho_out;       // [B, H, N, D] or null (then context-only attention)
+  const float* rho_in;  // [B, H, N, D] carried state, or null (zeros)
+  float* rho_out;       // [B, H, N, D] or null; == rho_in with T = 1: sparse decode step
   int64_t B, H, T, N, D;
   int64_t state_interval;  // state-carry interval when rho_out is set
 };

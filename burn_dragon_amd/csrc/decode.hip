@@ -2,12 +2,15 @@
 //   A = active rows of rot(x)   (x_i != 0, or x_{i^1} != 0 and frac(p f_i) != 0)
 //   a = rot(x)[A] . rho[A, :]   (read before the update)
 //   rho[A, :] += rot(x)[A]^T v
-// One 1024-thread workgroup per (batch, head) stream.  The workgroup
-// compacts the stream's active rows (8 rows per thread, wavefront prefix scan
-// with DPP shuffles, workgroup offsets through LDS) into an LDS list
-// (ascending), then its 16 waves stream exactly those rho rows: a whole
+// G 1024-thread workgroups per (batch, head) stream, each owning a range of
+// N / G rows (G grows while the grid stays within one workgroup per CU).
+// A workgroup compacts its range's active rows (8 rows per thread, wavefront
+// prefix scan with DPP shuffles, workgroup offsets through LDS) into an LDS
+// list (ascending), then its 16 waves stream exactly those rho rows: a whole
 // 1 KiB row per wave per load at D = 256 (float4 per lane), 8 rows in flight
-// per wave.  The readout is reduced across waves in LDS in a fixed order, so
+// per wave.  The readout is reduced across waves in LDS in a fixed order;
+// with G > 1 the range partials (and range lists) go to scratch and a
+// finalize kernel sums them (and concatenates the lists) in range order, so
 // results are deterministic and no atomics or cross-workgroup fences are
 // needed.  Rows outside A are never read or written.
 #include "bdh_internal.h"
@@ -26,10 +29,11 @@ struct DecodeKernelArgs {
   const float* v;
   float* rho;
   const float* freqs;
-  float* a_out;
-  int32_t* idx_out;
-  int32_t* cnt_out;
+  float* a_out;       // G == 1: [S, D]; else range partials [S, G, D]
+  int32_t* idx_out;   // G == 1: [S, N]; else range lists at their first row [S, N]
+  int32_t* cnt_out;   // G == 1: [S];    else range counts [S, G]
   int H, Hv, N, D;
+  int G, rows;        // ranges per stream, rows per range (a multiple of 8)
   float pos;
 };
 
@@ -53,12 +57,16 @@ __global__ __launch_bounds__(DR_THREADS) void decode_kernel(DecodeKernelArgs p) 
   __shared__ int32_t wtot[DR_WAVES];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t s = blockIdx.x;
+  const int64_t s = blockIdx.x / p.G;
+  const int g = (int)(blockIdx.x - s * p.G);
+  const int r0 = g * p.rows, r1 = min(p.N, r0 + p.rows);
   const int64_t b = s / p.H, h = s - b * p.H;
   const float* xs = p.x + s * p.N;
   const float* vs = p.v + (b * p.Hv + (p.Hv == 1 ? 0 : h)) * p.D;
   float* rho_s = p.rho + s * (int64_t)p.N * p.D;
   int done = 0;  // active rows listed so far (first column block only)
+  int32_t* idx_s = p.idx_out ? p.idx_out + s * p.N + (p.G > 1 ? r0 : 0) : nullptr;
+  float* a_s = p.a_out + (s * p.G + g) * p.D;
 
   for (int cb = 0; cb < p.D; cb += CB) {
     const bool first = cb == 0;
@@ -70,8 +78,8 @@ __global__ __launch_bounds__(DR_THREADS) void decode_kernel(DecodeKernelArgs p) 
       else vv.x = vs[c];
     }
 
-    for (int seg0 = 0; seg0 < p.N; seg0 += DR_SEG) {
-      const int seg_end = min(p.N, seg0 + DR_SEG);
+    for (int seg0 = r0; seg0 < r1; seg0 += DR_SEG) {
+      const int seg_end = min(r1, seg0 + DR_SEG);
       // ---- compaction of rows [seg0, seg_end) ----
       const int base = seg0 + tid * DR_ROWS_PER_THREAD;
       float r[DR_ROWS_PER_THREAD];
@@ -140,8 +148,8 @@ __global__ __launch_bounds__(DR_THREADS) void decode_kernel(DecodeKernelArgs p) 
         }
       __syncthreads();
       if (first) {
-        if (p.idx_out)
-          for (int k = tid; k < seg_total; k += DR_THREADS) p.idx_out[s * p.N + done + k] = lidx[k];
+        if (idx_s)
+          for (int k = tid; k < seg_total; k += DR_THREADS) idx_s[done + k] = lidx[k];
         done += seg_total;
       }
 
@@ -190,19 +198,51 @@ __global__ __launch_bounds__(DR_THREADS) void decode_kernel(DecodeKernelArgs p) 
       float sum = red[cc];
 #pragma unroll
       for (int w = 1; w < DR_WAVES; ++w) sum += red[w * CB + cc];
-      if (cb + cc < p.D) p.a_out[s * p.D + cb + cc] = sum;
+      if (cb + cc < p.D) a_s[cb + cc] = sum;
     }
     __syncthreads();
   }
-  if (p.idx_out)
-    for (int k = done + tid; k < p.N; k += DR_THREADS) p.idx_out[s * p.N + k] = -1;
-  if (p.cnt_out && tid == 0) p.cnt_out[s] = done;
+  if (p.G == 1 && idx_s)
+    for (int k = done + tid; k < p.N; k += DR_THREADS) idx_s[k] = -1;
+  if (p.cnt_out && tid == 0) p.cnt_out[s * p.G + g] = done;
+}
+
+// G > 1: a[s] = sum of the G range partials in range order; the range lists
+// concatenated (ascending overall), padded with -1, and their total count.
+__global__ __launch_bounds__(256) void decode_finalize_kernel(
+    const float* __restrict__ a_part, const int32_t* __restrict__ idx_part,
+    const int32_t* __restrict__ cnt_part, float* __restrict__ a_out, int32_t* __restrict__ idx_out,
+    int32_t* __restrict__ cnt_out, int G, int rows, int N, int D) {
+  const int64_t s = blockIdx.x;
+  const int tid = threadIdx.x;
+  for (int d = tid; d < D; d += 256) {
+    float sum = a_part[s * G * D + d];
+    for (int g = 1; g < G; ++g) sum += a_part[(s * G + g) * D + d];
+    a_out[s * D + d] = sum;
+  }
+  if (!cnt_part) return;
+  int off = 0;
+  for (int g = 0; g < G; ++g) {
+    const int c = cnt_part[s * G + g];
+    if (idx_out)
+      for (int k = tid; k < c; k += 256) idx_out[s * N + off + k] = idx_part[s * N + g * rows + k];
+    off += c;
+  }
+  if (idx_out)
+    for (int k = off + tid; k < N; k += 256) idx_out[s * N + k] = -1;
+  if (cnt_out && tid == 0) cnt_out[s] = off;
 }
 
 }  // namespace
 
 bdh_status run_decode(const DecodeArgs& a, hipStream_t st, uint64_t* launches) {
   const int64_t S = a.B * a.H;
+  // Ranges per stream: double while the grid stays within one workgroup per
+  // CU and a range keeps at least 256 rows.  (Measured: with a stream per CU
+  // already, splitting further costs more in partials than it gains.)
+  int G = 1;
+  while (G < 16 && S * 2 * G <= (int64_t)device_cus() && a.N / (2 * G) >= 256) G *= 2;
+  const int rows = (int)(((a.N + G - 1) / G + 7) / 8 * 8);
   DecodeKernelArgs p;
   p.x = a.x;
   p.v = a.v;
@@ -215,8 +255,26 @@ bdh_status run_decode(const DecodeArgs& a, hipStream_t st, uint64_t* launches) {
   p.Hv = (int)a.Hv;
   p.N = (int)a.N;
   p.D = (int)a.D;
+  p.G = G;
+  p.rows = rows;
   p.pos = a.pos;
-  const dim3 grid((unsigned)S);
+  if (G > 1) {
+    void *ap = nullptr, *ip = nullptr, *cp = nullptr;
+    bdh_status s = scratch(SLOT_DECODE_PART, (size_t)(S * G * a.D) * sizeof(float), &ap);
+    if (s != BDH_OK) return s;
+    p.a_out = (float*)ap;
+    if (a.idx_out) {
+      s = scratch(SLOT_DECODE_IDX, (size_t)(S * a.N) * sizeof(int32_t), &ip);
+      if (s != BDH_OK) return s;
+      p.idx_out = (int32_t*)ip;
+    }
+    if (a.idx_out || a.cnt_out) {
+      s = scratch(SLOT_DECODE_CNT, (size_t)(S * G) * sizeof(int32_t), &cp);
+      if (s != BDH_OK) return s;
+      p.cnt_out = (int32_t*)cp;
+    }
+  }
+  const dim3 grid((unsigned)(S * G));
   const bool vec4 = (a.D % 4) == 0;
   if (a.freqs) {
     if (vec4) hipLaunchKernelGGL((decode_kernel<true, true>), grid, dim3(DR_THREADS), 0, st, p);
@@ -225,9 +283,16 @@ bdh_status run_decode(const DecodeArgs& a, hipStream_t st, uint64_t* launches) {
     if (vec4) hipLaunchKernelGGL((decode_kernel<false, true>), grid, dim3(DR_THREADS), 0, st, p);
     else hipLaunchKernelGGL((decode_kernel<false, false>), grid, dim3(DR_THREADS), 0, st, p);
   }
-  if (launches) *launches += 1;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "decode_kernel launch");
+  if (launches) *launches += 1;
+  if (G > 1) {
+    hipLaunchKernelGGL(decode_finalize_kernel, dim3((unsigned)S), dim3(256), 0, st, p.a_out,
+                       p.idx_out, p.cnt_out, a.a_out, a.idx_out, a.cnt_out, G, rows, p.N, p.D);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "decode_finalize_kernel launch");
+    if (launches) *launches += 1;
+  }
   return BDH_OK;
 }
 

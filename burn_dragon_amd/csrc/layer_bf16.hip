@@ -30,6 +30,7 @@ struct LayerGemmArgs {
                       // L: lm_head [V, D]
   bf16_t* xy;         // X: x out; Y: x in, y out (same place); [B, H, T, N]
   bf16_t* q;          // X: rope(x) out [B, H, T, N], or null (no rotation)
+  float* xf;          // X: x out in f32 [B, H, T, N], or null
   const float* freqs; // X: RoPE frequencies [N] (with q)
   int64_t pos0;       // X: position of token 0
   int fixed;          // X: every token at pos0
@@ -165,6 +166,7 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
     const int64_t o = ((bb * g.H + h) * g.T + t) * g.N + n;
     const float r[4] = {fmaxf(v.x, 0.0f), fmaxf(v.y, 0.0f), fmaxf(v.z, 0.0f), fmaxf(v.w, 0.0f)};
     *reinterpret_cast<uint2*>(g.xy + o) = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+    if (g.xf) *reinterpret_cast<float4*>(g.xf + o) = make_float4(r[0], r[1], r[2], r[3]);
     if (g.q) {
       // q = rope(x) from the f32 activations: pairs (n, n+1), (n+2, n+3);
       // phase frac(p f) in the reference's f32 op order, cos / sin by
@@ -247,12 +249,28 @@ __global__ __launch_bounds__(256) void residual_kernel(const float* __restrict__
   const int lane = threadIdx.x & 63;
   if (m >= M) return;
   float v[LN_MAX];
+  const float* z = zpart + m * D + lane;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    float s = zpart[m * D + lane + 64 * i];
-    for (int kp = 1; kp < ks; ++kp) s += zpart[((int64_t)kp * M + m) * D + lane + 64 * i];
-    v[i] = s;
+  for (int i = 0; i < PER; ++i) v[i] = z[64 * i];
+  // Partials in order kp = 1, 2, ...; the loads of U splits are issued
+  // before their adds.
+  constexpr int U = PER <= 8 ? 4 : 1;
+  const int64_t zs = M * D;
+  int kp = 1;
+  for (; kp + U <= ks; kp += U) {
+    float t[U][PER];
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) t[j][i] = z[(kp + j) * zs + 64 * i];
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) v[i] += t[j][i];
   }
+  for (; kp < ks; ++kp)
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] += z[kp * zs + 64 * i];
   ln_wave<PER>(v, D);
 #pragma unroll
   for (int i = 0; i < PER; ++i) v[i] += cur[m * D + lane + 64 * i];
@@ -437,13 +455,17 @@ bdh_status lm_logits(const float* hidden, int64_t M, int64_t D, const bf16_t* he
 
 bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   const int64_t S = a.B * a.H, M = a.B * a.T, HN = a.H * a.N;
+  // One token carried in place: the sparse decode step touches only the rho
+  // rows of the token's active neurons, where the MFMA path would read and
+  // write all of rho.
+  const bool decode = a.T == 1 && a.rho_in != nullptr && a.rho_in == a.rho_out;
   void *curb = nullptr, *xy = nullptr, *attn = nullptr, *an = nullptr, *zp = nullptr;
   // Decoder split-K: the fewest splits (each an even number of 32-deep
-  // steps) that give at least two workgroups per CU.
+  // steps) that give at least two workgroups per CU, at most 64.
   const int64_t nkz = HN / 32;
   const int64_t tiles_z = (int64_t)cdiv(M, T256) * cdiv(a.D, T256 / 2);
   int ks = 1;
-  for (int cand = 1; cand <= 16 && nkz % (2 * cand) == 0; cand *= 2) {
+  for (int cand = 1; cand <= 64 && nkz % (2 * cand) == 0; cand *= 2) {
     ks = cand;
     if (tiles_z * cand >= 512) break;
   }
@@ -451,8 +473,13 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   if (s != BDH_OK) return s;
   s = scratch(SLOT_LAYER_XY, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xy);
   if (s != BDH_OK) return s;
+  // q: rope(x) in bf16 for the MFMA attention, or x in f32 for the decode
+  // step (which rotates as it gathers).
   void* q = nullptr;
-  if (a.freqs) {
+  if (decode) {
+    s = scratch(SLOT_LAYER_Q, (size_t)(S * a.N) * sizeof(float), &q);
+    if (s != BDH_OK) return s;
+  } else if (a.freqs) {
     s = scratch(SLOT_LAYER_Q, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &q);
     if (s != BDH_OK) return s;
   }
@@ -462,6 +489,15 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   if (s != BDH_OK) return s;
   s = scratch(SLOT_LAYER_Z, (size_t)(ks * M * a.D) * sizeof(float), &zp);
   if (s != BDH_OK) return s;
+  // A carried state whose successor is not kept still needs the state path
+  // (readout of rho_in); its rho goes to scratch.
+  float* rho_out = a.rho_out;
+  if (!decode && a.rho_in && !rho_out) {
+    void* r = nullptr;
+    s = scratch(SLOT_LAYER_RHO, (size_t)(S * a.N * a.D) * sizeof(float), &r);
+    if (s != BDH_OK) return s;
+    rho_out = (float*)r;
+  }
 
   hipLaunchKernelGGL(to_bf16_kernel, dim3(cdiv(M * a.D, 1024)), dim3(256), 0, st, a.cur,
                      (bf16_t*)curb, M * a.D);
@@ -474,31 +510,50 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   g.a = (const bf16_t*)curb;
   g.b = a.enc;
   g.xy = (bf16_t*)xy;
-  g.q = (bf16_t*)q;
+  g.q = decode ? nullptr : (bf16_t*)q;
+  g.xf = decode ? (float*)q : nullptr;
   g.freqs = a.freqs;
   g.pos0 = a.pos0;
   g.fixed = a.fixed;
   BDH_HIP_TRY(launch_gemm<G_X>(g, st));
   g.q = nullptr;
+  g.xf = nullptr;
 
-  // The attention reads the rotated queries GEMM X wrote (or x itself
-  // without RoPE), so it runs without a RoPE table.
-  Bf16Args b;
-  b.x = (const bf16_t*)(q ? q : xy);
-  b.v = (const bf16_t*)curb;
-  b.rho_in = nullptr;
-  b.decay = nullptr;
-  b.freqs = nullptr;
-  b.pos0 = 0;
-  b.fixed = 0;
-  b.ctx = (float*)attn;
-  b.rho_out = a.rho_out;
-  b.B = a.B; b.H = a.H; b.Hv = 1; b.T = a.T; b.N = a.N; b.D = a.D;
-  b.state = a.rho_out != nullptr;
-  b.L = b.state ? a.state_interval : ((a.T + 127) / 128) * 128;
   uint64_t n_attn = 0;
-  s = run_bf16_path(b, st, &n_attn);
-  if (s != BDH_OK) return s;
+  if (decode) {
+    // a = rope(x) . rho, then rho[A] += rope(x)[A]^T cur for the token's
+    // active set A, in f32 (value = the f32 layer input).
+    DecodeArgs d;
+    d.x = (const float*)q;
+    d.v = a.cur;
+    d.rho = a.rho_out;
+    d.freqs = a.freqs;
+    d.pos = (float)a.pos0;
+    d.a_out = (float*)attn;
+    d.idx_out = nullptr;
+    d.cnt_out = nullptr;
+    d.B = a.B; d.H = a.H; d.Hv = 1; d.N = a.N; d.D = a.D;
+    s = run_decode(d, st, &n_attn);
+    if (s != BDH_OK) return s;
+  } else {
+    // The attention reads the rotated queries GEMM X wrote (or x itself
+    // without RoPE), so it runs without a RoPE table.
+    Bf16Args b;
+    b.x = (const bf16_t*)(q ? q : xy);
+    b.v = (const bf16_t*)curb;
+    b.rho_in = a.rho_in;
+    b.decay = nullptr;
+    b.freqs = nullptr;
+    b.pos0 = 0;
+    b.fixed = 0;
+    b.ctx = (float*)attn;
+    b.rho_out = rho_out;
+    b.B = a.B; b.H = a.H; b.Hv = 1; b.T = a.T; b.N = a.N; b.D = a.D;
+    b.state = rho_out != nullptr;
+    b.L = b.state ? a.state_interval : ((a.T + 127) / 128) * 128;
+    s = run_bf16_path(b, st, &n_attn);
+    if (s != BDH_OK) return s;
+  }
 
   BDH_HIP_TRY(dispatch_per<LnF>((int)a.D, (const float*)attn, (bf16_t*)an, S * a.T, (int)a.D, st));
   g.a = (const bf16_t*)an;

@@ -247,27 +247,31 @@ __global__ __launch_bounds__(256) void rope_table_bf16_kernel(const float* __res
   cs[i] = pack_bf16x2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
 }
 
-// q[s, t, :] = rope(x[s, t, :]) in bf16, 8 elements (4 pairs) per thread:
-// phase frac(p f) in the reference's f32 op order, cos / sin by v_cos_f32 /
-// v_sin_f32 of it, the rotation in f32 in the op order of
-// attention.rs:488-501, then rounded to bf16.
+// q[s, t, :] = rope(x[s, t, :]) in bf16: phase frac(p f) in the reference's
+// f32 op order, cos / sin by v_cos_f32 / v_sin_f32 of it, the rotation in f32
+// in the op order of attention.rs:488-501, then rounded to bf16.  Workgroup b
+// covers 2048 elements (8 a lane) of row row0 + b / segs, so the row and its
+// position are workgroup-uniform (scalar arithmetic).
+constexpr int ROT_SEG = 2048;
 __global__ __launch_bounds__(256) void rope_rotate_bf16_kernel(const bf16_t* __restrict__ x,
                                                                const float* __restrict__ freqs,
-                                                               bf16_t* __restrict__ q, int64_t rows,
-                                                               int64_t T, int64_t N,
+                                                               bf16_t* __restrict__ q, int64_t row0,
+                                                               int64_t segs, int64_t T, int64_t N,
                                                                int64_t pos_first, int fixed) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 8-element chunk
-  const int64_t per_row = N / 8;
-  if (i >= rows * per_row) return;
-  const int64_t row = i / per_row, n = (i - row * per_row) * 8;
-  const int64_t t = row % T;
-  const float p = (float)(fixed ? pos_first : pos_first + t);
+  const int64_t b = blockIdx.x / segs;
+  const int64_t n = (blockIdx.x - b * segs) * ROT_SEG + threadIdx.x * 8;
+  const int64_t row = row0 + b;
+  if (n >= N) return;  // N % 8 == 0: a lane's 8 elements are all in the row or all past it
+  const float p = (float)(fixed ? pos_first : pos_first + row % T);
   const uint4 raw = *reinterpret_cast<const uint4*>(x + row * N + n);
+  const float4 f0 = *reinterpret_cast<const float4*>(freqs + n);
+  const float4 f1 = *reinterpret_cast<const float4*>(freqs + n + 4);
   const uint32_t in[4] = {raw.x, raw.y, raw.z, raw.w};
+  const float f[4] = {f0.x, f0.z, f1.x, f1.z};  // one frequency per pair
   uint32_t out[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const float fr = rope_frac(p, freqs[n + 2 * k]);
+    const float fr = rope_frac(p, f[k]);
     float e, o;
     rope_pair_exact(bf16_lo(in[k]), bf16_hi(in[k]), __builtin_amdgcn_cosf(fr),
                     __builtin_amdgcn_sinf(fr), e, o);
@@ -391,10 +395,16 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   uint64_t n_launch = 1;
   BDH_HIP_TRY(hipGetLastError());
   if (prerot) {
-    hipLaunchKernelGGL(rope_rotate_bf16_kernel, dim3(cdiv(S * a.T * (a.N / 8), 256)), dim3(256), 0,
-                       st, a.x, a.freqs, (bf16_t*)xr, S * a.T, a.T, a.N, a.pos0, a.fixed);
-    BDH_HIP_TRY(hipGetLastError());
-    ++n_launch;
+    // Launches of at most 2^22 workgroups (2^30 work-items) each.
+    const int64_t segs = cdiv(a.N, ROT_SEG);
+    const int64_t rows_per = ((int64_t)1 << 22) / segs;
+    for (int64_t r0 = 0; r0 < S * a.T; r0 += rows_per) {
+      const int64_t rows = S * a.T - r0 < rows_per ? S * a.T - r0 : rows_per;
+      hipLaunchKernelGGL(rope_rotate_bf16_kernel, dim3((unsigned)(rows * segs)), dim3(256), 0, st,
+                         a.x, a.freqs, (bf16_t*)xr, r0, segs, a.T, a.N, a.pos0, a.fixed);
+      BDH_HIP_TRY(hipGetLastError());
+      ++n_launch;
+    }
   } else if (rope) {
     hipLaunchKernelGGL(rope_table_bf16_kernel, dim3(cdiv(a.T * half, 256)), dim3(256), 0, st,
                        a.freqs, (uint32_t*)cs, a.T, half, a.pos0, a.fixed);

@@ -69,10 +69,15 @@ class LowRankLayerOutput(NamedTuple):
 
 def lowrank_layer_forward(current: torch.Tensor, weights: LowRankWeights, *,
                           position: Optional[int] = 0, theta: float = DEFAULT_ROPE_THETA,
-                          want_rho: bool = False, out: Optional[torch.Tensor] = None
+                          want_rho: bool = False, out: Optional[torch.Tensor] = None,
+                          rho: Optional[torch.Tensor] = None, inplace: bool = False
                           ) -> Optional[LowRankLayerOutput]:
     """current [B,1,T,D] or [B,T,D] f32 on the device; ``position`` is the
-    first token's RoPE position (None: no rotation).  Returns None where the
+    first token's RoPE position (None: no rotation).  ``rho`` [B,H,N,D] f32
+    is the layer's carried state (None: zeros).  With ``inplace`` the
+    successor state is written over ``rho`` (the model's per-layer state;
+    a single token then takes the sparse decode step); otherwise it is
+    returned in a new tensor when ``want_rho``.  Returns None where the
     library does not support the shape."""
     if not supports_backend() or weights is None:
         return None
@@ -84,16 +89,30 @@ def lowrank_layer_forward(current: torch.Tensor, weights: LowRankWeights, *,
         return None
     H, N = weights.heads, weights.latent
     cur = cur.contiguous()
+    if rho is not None:
+        if (tuple(rho.shape) != (B, H, N, D) or rho.dtype != torch.float32 or not rho.is_cuda
+                or (inplace and not rho.is_contiguous())):
+            return None
+        rho_in = rho.contiguous()
+    elif inplace:
+        return None
+    else:
+        rho_in = None
     nxt = out if out is not None else torch.empty((B, T, D), device=cur.device, dtype=torch.float32)
-    rho = torch.empty((B, H, N, D), device=cur.device, dtype=torch.float32) if want_rho else None
+    if inplace:
+        rho_out = rho_in
+    elif want_rho:
+        rho_out = torch.empty((B, H, N, D), device=cur.device, dtype=torch.float32)
+    else:
+        rho_out = None
     plan = _lib.BdhLayerPlan(B, H, T, N, D)
     rope = None
     if position is not None:
         rope = _lib.BdhRope(_lib.BDH_ROPE_SEQUENTIAL, 0, int(position), float(theta))
     st = _lib.load().bdh_lowrank_layer_fwd(
         ctypes.byref(plan), _ptr(cur), _ptr(weights.encoder), _ptr(weights.encoder_v),
-        _ptr(weights.decoder), ctypes.byref(rope) if rope else None, _ptr(nxt), _ptr(rho),
-        ctypes.c_void_p(_stream_ptr(cur.device)))
+        _ptr(weights.decoder), ctypes.byref(rope) if rope else None, _ptr(rho_in), _ptr(nxt),
+        _ptr(rho_out), ctypes.c_void_p(_stream_ptr(cur.device)))
     if not _lib.check(st):
         return None
-    return LowRankLayerOutput(nxt, rho)
+    return LowRankLayerOutput(nxt, rho_out)

@@ -138,9 +138,17 @@ bdh_status bdh_dense_causal_attention_fwd(const bdh_recurrent_plan* plan, int32_
  *   next = LN(cur + LN(decode_y_neuron_tail(y, Dec)))   (:309-321)
  * LN = DragonNorm LayerNorm with gamma = 1, beta = 0, eps = 1e-5 (norm.rs:302-328).
  * current, next_out [B,T,D] f32 (Burn's [B,1,T,D]); weights packed by
- * bdh_lowrank_pack_weights; rope may be NULL (no rotation); rho_out
- * [B,H,N,D] f32, or NULL when the terminal state is not retained.
- * Needs latent % 256 == 0 and embd % 64 == 0, embd <= 2048. */
+ * bdh_lowrank_pack_weights; rope may be NULL (no rotation).
+ * rho_in [B,H,N,D] f32 is the layer's carried state (LayerState.rho, read
+ * by recurrent_attention_with_plan, sequence_dispatch.rs:83-136; dragon.rs
+ * :3437-3446 passes each layer its own state), NULL = zeros.  rho_out
+ * [B,H,N,D] f32 receives the successor state, or NULL when it is not
+ * retained; it may equal rho_in (in place).  With time == 1 and
+ * rho_out == rho_in the attention is the sparse decode step of
+ * bdh_decode_step (only the rho rows of the token's active neurons are
+ * read and written); otherwise it is the MFMA prefill path.
+ * Needs latent % 256 == 0 and embd % 64 == 0, embd <= 2048; all pointers
+ * 16-byte aligned. */
 typedef struct {
   int64_t batch, heads, time, latent, embd;
 } bdh_layer_plan;
@@ -159,7 +167,8 @@ bdh_status bdh_lowrank_pack_weights(int64_t heads, int64_t latent, int64_t embd,
 bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* current,
                                  const void* encoder_packed, const void* encoder_v_packed,
                                  const void* decoder_packed, const bdh_rope* rope,
-                                 float* next_out, float* rho_out, void* stream);
+                                 const float* rho_in, float* next_out, float* rho_out,
+                                 void* stream);
 
 /* The model's input: out = LN(embed[token]) per token, the embedding lookup
  * followed by DragonModel's input norm (dragon.rs:3352, norm.rs:302-328).

@@ -235,17 +235,25 @@ def lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=0, theta: float = 6
 
 
 def model_forward_f64(tokens, embed, encoder, encoder_v, decoder, lm_head, n_layer: int,
-                      pos0=0, theta: float = 65536.0) -> np.ndarray:
+                      pos0=0, theta: float = 65536.0, rho0s=None, return_state: bool = False):
     """DragonModel sequence forward with shared low-rank weights and the
     vanilla residual connector (dragon.rs:3340-3420): current =
     LN(embed[tokens]) (:3352), n_layer x lowrank_layer_f64 with the same
     positions, then logits = current @ lm_head (project_hidden_to_logits,
-    :4033-4055).  tokens [B,T]; returns logits [B,T,vocab] f64."""
+    :4033-4055).  tokens [B,T]; returns logits [B,T,vocab] f64.
+    rho0s: per-layer carried states (each layer's LayerState.rho,
+    dragon.rs:3437-3446), None = zeros; with return_state the per-layer
+    successor states are returned too."""
     emb = np.asarray(embed, np.float64)
     cur = layer_norm_f64(emb[np.asarray(tokens)])
-    for _ in range(n_layer):
-        cur, _ = lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=pos0, theta=theta)
-    return cur @ np.asarray(lm_head, np.float64)
+    rhos = []
+    for layer in range(n_layer):
+        rho0 = rho0s[layer] if rho0s is not None else None
+        cur, rho = lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=pos0, theta=theta,
+                                     rho0=rho0)
+        rhos.append(rho)
+    logits = cur @ np.asarray(lm_head, np.float64)
+    return (logits, rhos) if return_state else logits
 
 
 def rel_l2(a, b) -> float:

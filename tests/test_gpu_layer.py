@@ -114,3 +114,71 @@ def test_model_forward_matches_oracle(oracle):
     e = rel_l2(host(logits), ref)
     print(f"rel-L2 logits {e:.2e}")
     assert e <= TOL_BF16
+
+
+@pytest.mark.parametrize("B,H,T,N,D,pos,mode", [
+    (2, 2, 150, 256, 64, 7, "copy"),       # carried rho in, successor to a new buffer
+    (1, 2, 600, 256, 128, 3, "inplace"),   # two state intervals, successor over rho
+    (2, 2, 100, 256, 64, 4, "nokeep"),     # carried rho, successor not kept
+    (3, 2, 1, 512, 128, 9, "inplace"),     # one token in place: the sparse decode step
+    (3, 2, 1, 512, 128, 9, "copy"),        # one token to a new buffer: the MFMA path
+])
+def test_layer_carried_state_matches_oracle(oracle, B, H, T, N, D, pos, mode):
+    # LayerState.rho in (sequence_dispatch.rs:83-136): the attention starts
+    # from rho0 instead of zeros.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(B * 100 + T + N + D)
+    cur, enc, encv, dec = _case(rng, B, H, T, N, D)
+    rho0 = (rng.standard_normal((B, H, N, D)) * 0.05).astype(np.float32)
+    w = bd.LowRankWeights.pack(dev(torch, enc[None]), dev(torch, encv[None]), dev(torch, dec))
+    rho_t = dev(torch, rho0)
+    announce("layer carried state", B, H, T, N, D, pos, mode)
+    out = bd.lowrank_layer_forward(dev(torch, cur), w, position=pos, rho=rho_t,
+                                   inplace=mode == "inplace", want_rho=mode == "copy")
+    torch.cuda.synchronize()
+    assert out is not None
+    nref, rref = oracle.lowrank_layer_f64(cur, oracle.round_bf16(enc), oracle.round_bf16(encv),
+                                          oracle.round_bf16(dec), pos0=pos, rho0=rho0)
+    e_next = rel_l2(host(out.next), nref)
+    msg = f"rel-L2 next {e_next:.2e}"
+    if mode == "nokeep":
+        assert out.rho is None
+    else:
+        e_rho = rel_l2(host(out.rho), rref)
+        msg += f" rho {e_rho:.2e}"
+        assert e_rho <= TOL_BF16, msg
+    if mode != "inplace":
+        assert np.array_equal(host(rho_t), rho0)  # the caller's state is not written
+    print(msg)
+    assert e_next <= TOL_BF16, msg
+
+
+def test_model_prompt_then_decode_matches_oracle(oracle):
+    # A prompt through forward_with_state, then one token per call carrying
+    # every layer's rho and the position (the generation loop), against one
+    # oracle forward over the whole sequence.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(91)
+    B, T0, steps, V, D, H, N, L = 2, 40, 3, 256, 64, 2, 256, 2
+    _, enc, encv, dec = _case(rng, 1, H, 1, N, D)
+    embed = (rng.standard_normal((V, D)) * 0.02).astype(np.float32)
+    head = (rng.standard_normal((D, V)) * 0.02).astype(np.float32)
+    tokens = rng.integers(0, V, (B, T0 + steps)).astype(np.int32)
+    w = bd.pack_model(dev(torch, embed), dev(torch, enc[None]), dev(torch, encv[None]),
+                      dev(torch, dec), dev(torch, head), L)
+    tok = dev(torch, tokens)
+    state = bd.new_model_state(w, B, tok.device)
+    announce("model prompt + decode", B, T0, steps, V, D, H, N, L)
+    parts = [bd.model_forward_logits(tok[:, :T0], w, state=state)]
+    for t in range(T0, T0 + steps):
+        parts.append(bd.model_forward_logits(tok[:, t:t + 1], w, state=state))
+    torch.cuda.synchronize()
+    assert all(p is not None for p in parts) and state.position == T0 + steps
+    got = np.concatenate([host(p) for p in parts], axis=1)
+    ref = oracle.model_forward_f64(tokens, embed, oracle.round_bf16(enc), oracle.round_bf16(encv),
+                                   oracle.round_bf16(dec), oracle.round_bf16(head), L)
+    e_all, e_steps = rel_l2(got, ref), rel_l2(got[:, T0:], ref[:, T0:])
+    print(f"rel-L2 logits {e_all:.2e}, decoded tokens {e_steps:.2e}")
+    assert e_all <= TOL_BF16 and e_steps <= TOL_BF16

@@ -115,6 +115,7 @@ def _bf16_case(rng, B, H, Hv, T, N, D, with_rho):
     (1, 2, 1, 1100, 256, 128, True, None, 3),         # 3 state intervals (512+512+76)
     (1, 4, 1, 256, 256, 64, True, [0.99, 0.98, 0.97, 0.96], 0),  # ALiBi-style decay
     (1, 2, 1, 700, 512, 320, True, [0.995, 0.99], 9),  # D > 256, not a multiple of 256; 2 intervals
+    (2, 2, 1, 600, 2304, 64, False, None, 5),          # x rotated once: rows of 4 streams, N % 2048 != 0
 ])
 def test_bf16_rope_prefill_matches_oracle(oracle, B, H, Hv, T, N, D, with_rho, decay, pos):
     torch = need_gpu()
@@ -132,14 +133,15 @@ def test_bf16_rope_prefill_matches_oracle(oracle, B, H, Hv, T, N, D, with_rho, d
     assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
 
 
-def test_bf16_rope_fixed_mode(oracle):
+@pytest.mark.parametrize("T", [384, 1100])  # one interval (table path); three (x rotated once)
+def test_bf16_rope_fixed_mode(oracle, T):
     # rotate_positions_fixed (attention.rs:512-550): every token at one position.
     torch = need_gpu()
     import burn_dragon_amd as bd
     rng = np.random.default_rng(41)
-    x, v, rho0 = _bf16_case(rng, 1, 2, 1, 384, 256, 64, True)
+    x, v, rho0 = _bf16_case(rng, 1, 2, 1, T, 256, 64, True)
     xb, vb = oracle.round_bf16(x), oracle.round_bf16(v)
-    announce("bf16 rope fixed", 1, 2, 384, 256, 64)
+    announce("bf16 rope fixed", 1, 2, T, 256, 64)
     ctx, rho = _run(torch, bd, xb, vb, rho0, None, dtype=torch.bfloat16, rope=(1000, True))
     q = oracle.rope_rotate(xb, pos0=1000, mode=1)
     cref, rref = oracle.recurrent_f64(q, vb, rho0)

@@ -125,3 +125,36 @@ def test_model_oracle_composition(oracle):
     # zero layers: logits of the normalised embeddings only
     got0 = oracle.model_forward_f64(tokens, embed, enc, encv, dec, head, 0)
     assert np.max(np.abs(got0[0] - cur[0] @ head)) < 1e-12
+
+
+def test_model_state_carry_splits_a_sequence(oracle):
+    # forward_with_state over a prompt, then one token at a time carrying each
+    # layer's rho and the position (dragon.rs:3334, :3437-3446), equals one
+    # forward over the whole sequence.  Dropping the carried state or not
+    # advancing the position must break it.
+    rng = np.random.default_rng(13)
+    V, D, H, N, T, L = 7, 8, 2, 8, 5, 2
+    embed = rng.standard_normal((V, D))
+    enc = rng.standard_normal((H, D, N)) * 0.5
+    encv = rng.standard_normal((H, D, N)) * 0.5
+    dec = rng.standard_normal((H * N, D)) * 0.5
+    head = rng.standard_normal((D, V))
+    tokens = rng.integers(0, V, (2, T))
+    whole = oracle.model_forward_f64(tokens, embed, enc, encv, dec, head, L, pos0=0)
+
+    def split(carry=True, advance=True):
+        out, rhos = oracle.model_forward_f64(tokens[:, :3], embed, enc, encv, dec, head, L,
+                                             pos0=0, return_state=True)
+        steps = [out]
+        for t in range(3, T):
+            lg, new = oracle.model_forward_f64(tokens[:, t:t + 1], embed, enc, encv, dec, head, L,
+                                               pos0=t if advance else 0,
+                                               rho0s=rhos if carry else None, return_state=True)
+            steps.append(lg)
+            rhos = new
+        return np.concatenate(steps, axis=1)
+
+    scale = np.max(np.abs(whole))
+    assert np.max(np.abs(split() - whole)) < 1e-5 * scale
+    assert np.max(np.abs(split(carry=False) - whole)) > 1e-2 * scale
+    assert np.max(np.abs(split(advance=False) - whole)) > 1e-2 * scale
