@@ -194,6 +194,118 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
   for (int id = blockIdx.x; id < total; id += gridDim.x) gemm_tile<KIND>(g, lds, id);
 }
 
+// ---- few-row GEMMs (M <= 64 token rows, e.g. one generated token per
+// sequence) ---------------------------------------------------------------
+// The 256 x 128 tile would run 8 (K = 256) or more dependent 32-deep steps on
+// mostly empty rows.  Here a workgroup owns one 16-column block and a K
+// range; its 4 waves split the range, each loading its steps' operands
+// straight into MFMA fragment registers (8 steps' loads in flight, no LDS
+// staging), and sum their accumulators through LDS in wave order.  Up to 4
+// 16-row blocks; rows past M re-read row M - 1 and are never stored.
+constexpr int SK_MAXM = 64;
+constexpr int SK_CHUNK = 8;  // 32-deep steps loaded at once per wave
+
+template <int KIND, int MB>  // MB = 16-row blocks: 1, 2 or 4
+__global__ __launch_bounds__(256) void skinny_gemm_kernel(LayerGemmArgs g) {
+  __shared__ floatx4 red[4][MB][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t ncols = KIND == G_Z ? g.D : KIND == G_L ? g.V : g.H * g.N;
+  const int64_t K = KIND == G_Z ? g.H * g.N : g.D;
+  const int ncb = (int)((ncols + 15) / 16);
+  const int cblk = (int)(blockIdx.x % ncb), kp = (int)(blockIdx.x / ncb);
+  const int64_t c0 = (int64_t)cblk * 16;
+  const int64_t h = (KIND == G_X || KIND == G_Y) ? c0 / g.N : 0;
+  // Steps of this wave: part p of 4 * ks equal parts of the K/32 steps.
+  const int64_t nk = K / 32, parts = 4 * (int64_t)g.ks, p = (int64_t)kp * 4 + w;
+  const int kb = (int)(nk * p / parts), ke = (int)(nk * (p + 1) / parts);
+
+  const int kl = 8 * (lane >> 4);  // this lane's 8 k values within a step
+  int64_t cb = c0 + (lane & 15);
+  cb = cb < ncols ? cb : ncols - 1;
+  const bf16_t* brow = g.b + cb * K + kl;
+  const bf16_t* arow[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    int64_t m = 16 * mb + (lane & 15);
+    m = m < g.M ? m : g.M - 1;
+    const int64_t bb = m / g.T, t = m - bb * g.T;
+    if (KIND == G_X || KIND == G_L) arow[mb] = g.a + m * g.D + kl;
+    else if (KIND == G_Y) arow[mb] = g.a + ((bb * g.H + h) * g.T + t) * g.D + kl;
+    else arow[mb] = g.a + (bb * g.H * g.T + t) * g.N + kl;
+  }
+  floatx4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = zero4();
+  for (int k0 = kb; k0 < ke; k0 += SK_CHUNK) {
+    const int n = ke - k0 < SK_CHUNK ? ke - k0 : SK_CHUNK;
+    bf16x8 bq[SK_CHUNK], aq[SK_CHUNK][MB];
+#pragma unroll
+    for (int s = 0; s < SK_CHUNK; ++s) {
+      if (s >= n) break;
+      const int64_t k = (int64_t)(k0 + s) * 32;
+      // Z: k runs over (head, neuron); a 32-deep step stays inside one head.
+      const int64_t aoff = KIND == G_Z ? (k / g.N) * g.T * g.N + k % g.N : k;
+      bq[s] = *reinterpret_cast<const bf16x8*>(brow + k);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) aq[s][mb] = *reinterpret_cast<const bf16x8*>(arow[mb] + aoff);
+    }
+#pragma unroll
+    for (int s = 0; s < SK_CHUNK; ++s) {
+      if (s >= n) break;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16(aq[s][mb], bq[s], acc[mb]);
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) red[w][mb][lane] = acc[mb];
+  __syncthreads();
+  // Wave mb finishes row block mb: the 4 wave partials in order, then the
+  // epilogue of the 16 x 16 block (lane: rows 4 (lane >> 4) + r, column
+  // lane & 15).
+  const int mb = w;
+  if (mb >= MB) return;
+  floatx4 v = red[0][mb][lane];
+#pragma unroll
+  for (int ww = 1; ww < 4; ++ww) v = v + red[ww][mb][lane];
+  const int64_t c = c0 + (lane & 15);
+  const int64_t n = c - h * g.N;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t m = 16 * mb + acc16_row(lane, r);
+    float val = v[r];
+    if (KIND == G_X) {
+      // Every lane joins the partner exchange before any row test.
+      const float x = fmaxf(val, 0.0f);
+      const float xp = __shfl_xor(x, 1, 64);  // column c ^ 1 of the same row
+      if (m >= g.M) continue;
+      const int64_t bb = m / g.T, t = m - bb * g.T;
+      const int64_t o = ((bb * g.H + h) * g.T + t) * g.N + n;
+      g.xy[o] = (bf16_t)x;
+      if (g.xf) g.xf[o] = x;
+      if (g.q) {
+        const float p = (float)(g.fixed ? g.pos0 : g.pos0 + t);
+        const int64_t ne = n & ~(int64_t)1;
+        const float fr = rope_frac(p, g.freqs[ne]);
+        const float e = (n & 1) ? xp : x, od = (n & 1) ? x : xp;
+        float qe, qo;
+        rope_pair_exact(e, od, __builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr), qe, qo);
+        g.q[o] = (bf16_t)((n & 1) ? qo : qe);
+      }
+    } else {
+      if (m >= g.M) continue;
+      if (KIND == G_Y) {
+        const int64_t bb = m / g.T, t = m - bb * g.T;
+        bf16_t* dst = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
+        *dst = (bf16_t)(fmaxf(val, 0.0f) * (float)*dst);
+      } else if (KIND == G_Z) {
+        g.zpart[((int64_t)kp * g.M + m) * g.D + c] = val;
+      } else if (c < g.V) {
+        g.zpart[m * g.V + c] = val;
+      }
+    }
+  }
+}
+
 // Wave-wide sum (fixed butterfly order: the same result in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -332,8 +444,21 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const float* __rest
 
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
+// Few-row GEMM launch: one workgroup per (16-column block, K split).
+template <int KIND>
+hipError_t launch_skinny(const LayerGemmArgs& g, hipStream_t st) {
+  const int64_t ncols = KIND == G_Z ? g.D : KIND == G_L ? g.V : g.H * g.N;
+  const int64_t blocks = cdiv(ncols, 16) * (int64_t)(KIND == G_Z ? g.ks : 1);
+  const dim3 grid((unsigned)blocks);
+  if (g.M <= 16) hipLaunchKernelGGL((skinny_gemm_kernel<KIND, 1>), grid, dim3(256), 0, st, g);
+  else if (g.M <= 32) hipLaunchKernelGGL((skinny_gemm_kernel<KIND, 2>), grid, dim3(256), 0, st, g);
+  else hipLaunchKernelGGL((skinny_gemm_kernel<KIND, 4>), grid, dim3(256), 0, st, g);
+  return hipGetLastError();
+}
+
 template <int KIND>
 hipError_t launch_gemm(const LayerGemmArgs& g, hipStream_t st) {
+  if (g.M <= SK_MAXM) return launch_skinny<KIND>(g, st);
   const int64_t total = (int64_t)g.mt * g.ct * (KIND == G_Z ? g.ks : 1);
   const int64_t slots = 2 * (int64_t)device_cus();  // two workgroups per CU
   const unsigned grid = (unsigned)(total < slots ? total : slots);
@@ -460,14 +585,19 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   // write all of rho.
   const bool decode = a.T == 1 && a.rho_in != nullptr && a.rho_in == a.rho_out;
   void *curb = nullptr, *xy = nullptr, *attn = nullptr, *an = nullptr, *zp = nullptr;
-  // Decoder split-K: the fewest splits (each an even number of 32-deep
-  // steps) that give at least two workgroups per CU, at most 64.
+  // Decoder split-K.  256 x 128 tiles: the fewest splits (each an even
+  // number of 32-deep steps) that give at least two workgroups per CU, at
+  // most 16.  Few rows: about 8 steps per wave (32 per workgroup), at most 64.
   const int64_t nkz = HN / 32;
-  const int64_t tiles_z = (int64_t)cdiv(M, T256) * cdiv(a.D, T256 / 2);
   int ks = 1;
-  for (int cand = 1; cand <= 64 && nkz % (2 * cand) == 0; cand *= 2) {
-    ks = cand;
-    if (tiles_z * cand >= 512) break;
+  if (M <= SK_MAXM) {
+    while (ks < 64 && nkz / (2 * ks) >= 32) ks *= 2;
+  } else {
+    const int64_t tiles_z = (int64_t)cdiv(M, T256) * cdiv(a.D, T256 / 2);
+    for (int cand = 1; cand <= 16 && nkz % (2 * cand) == 0; cand *= 2) {
+      ks = cand;
+      if (tiles_z * cand >= 512) break;
+    }
   }
   bdh_status s = scratch(SLOT_LAYER_CUR, (size_t)(M * a.D) * sizeof(bf16_t), &curb);
   if (s != BDH_OK) return s;
