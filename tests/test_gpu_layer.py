@@ -22,6 +22,8 @@ def _case(rng, B, H, T, N, D):
     (2, 2, 200, 256, 64, 5, False),     # ragged rows (M = 400), context-only attention
     (1, 4, 300, 512, 128, 0, True),     # rho out: one 300-token state interval
     (1, 2, 640, 256, 256, 17, True),    # two state intervals (512 + 128), D = 256
+    (1, 2, 24, 256, 64, 11, True),      # few-row GEMMs, two 16-row blocks
+    (3, 2, 16, 512, 128, 2, False),     # few-row GEMMs, four 16-row blocks (M = 48)
 ])
 def test_layer_matches_oracle(oracle, B, H, T, N, D, pos, want_rho):
     torch = need_gpu()
