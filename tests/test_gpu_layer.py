@@ -156,6 +156,35 @@ def test_layer_carried_state_matches_oracle(oracle, B, H, T, N, D, pos, mode):
     assert e_next <= TOL_BF16, msg
 
 
+def test_model_incremental_matches_full_sequence(oracle):
+    # linear_attention_incremental_forward_matches_full_sequence
+    # (dragon.rs:5028-5057): tokens 1..6 one per forward_with_state call from
+    # the initial state equal the full-sequence forward; position ends at 6.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(92)
+    V, D, H, N, L = 256, 64, 2, 256, 2
+    _, enc, encv, dec = _case(rng, 1, H, 1, N, D)
+    embed = (rng.standard_normal((V, D)) * 0.02).astype(np.float32)
+    head = (rng.standard_normal((D, V)) * 0.02).astype(np.float32)
+    tokens = np.array([[1, 2, 3, 4, 5, 6]], np.int32)
+    w = bd.pack_model(dev(torch, embed), dev(torch, enc[None]), dev(torch, encv[None]),
+                      dev(torch, dec), dev(torch, head), L)
+    tok = dev(torch, tokens)
+    announce("model incremental vs full", V, D, H, N, L)
+    full = bd.model_forward_logits(tok, w, position=0)
+    state = bd.new_model_state(w, 1, tok.device)
+    pieces = [bd.model_forward_logits(tok[:, i:i + 1], w, state=state) for i in range(6)]
+    torch.cuda.synchronize()
+    assert state.position == 6
+    inc = np.concatenate([host(p) for p in pieces], axis=1)
+    ref = oracle.model_forward_f64(tokens, embed, oracle.round_bf16(enc), oracle.round_bf16(encv),
+                                   oracle.round_bf16(dec), oracle.round_bf16(head), L)
+    e_full, e_inc, e_pair = rel_l2(host(full), ref), rel_l2(inc, ref), rel_l2(inc, host(full))
+    print(f"rel-L2 full {e_full:.2e}, incremental {e_inc:.2e}, incremental vs full {e_pair:.2e}")
+    assert e_full <= TOL_BF16 and e_inc <= TOL_BF16 and e_pair <= TOL_BF16
+
+
 def test_model_prompt_then_decode_matches_oracle(oracle):
     # A prompt through forward_with_state, then one token per call carrying
     # every layer's rho and the position (the generation loop), against one

@@ -130,7 +130,9 @@ def test_model_oracle_composition(oracle):
 def test_model_state_carry_splits_a_sequence(oracle):
     # forward_with_state over a prompt, then one token at a time carrying each
     # layer's rho and the position (dragon.rs:3334, :3437-3446), equals one
-    # forward over the whole sequence.  Dropping the carried state or not
+    # forward over the whole sequence: the invariant of the reference's
+    # linear_attention_incremental_forward_matches_full_sequence
+    # (dragon.rs:5028-5057).  Dropping the carried state or not
     # advancing the position must break it.
     rng = np.random.default_rng(13)
     V, D, H, N, T, L = 7, 8, 2, 8, 5, 2
