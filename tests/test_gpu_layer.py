@@ -24,6 +24,8 @@ def _case(rng, B, H, T, N, D):
     (1, 2, 640, 256, 256, 17, True),    # two state intervals (512 + 128), D = 256
     (1, 2, 24, 256, 64, 11, True),      # few-row GEMMs, two 16-row blocks
     (3, 2, 16, 512, 128, 2, False),     # few-row GEMMs, four 16-row blocks (M = 48)
+    (1, 1, 40, 256, 2048, 3, True),     # widest embd: 32 values a lane in the LayerNorms
+    (2, 1, 160, 256, 1024, 0, False),   # wide embd on the 256 x 128 tiles (M = 320)
 ])
 def test_layer_matches_oracle(oracle, B, H, T, N, D, pos, want_rho):
     torch = need_gpu()
