@@ -25,7 +25,7 @@ namespace {
 
 constexpr int CK = 32;         // k step of the context kernel: 64-byte LDS rows
 constexpr int CTX_ROWS = 64;   // output rows of one workgroup
-constexpr int CTX_COLS = 256;  // output columns of one workgroup (4 waves x 64)
+constexpr int CTX_COLS = 256;  // output columns of a wide workgroup (4 waves x 64); narrow: 128
 
 // Element offset of 16-byte chunk c (0..3) of a 64-byte LDS row r, XOR
 // swizzled with bits 1..2 of the row: conflict-free for MFMA fragment reads
@@ -47,9 +47,11 @@ struct CtxArgs {
 
 // Workgroup id -> (row block, interval, stream): row blocks heaviest first
 // (row block rb contracts over 64 (rb + 1) columns), then interval, then
-// stream.  blockIdx.y is the 256-column block.
-template <int KS>
+// stream.  blockIdx.y is the column block: 4 waves x WC columns (WC = 64, or
+// 32 when the wide blocks would leave CUs with fewer than two workgroups).
+template <int KS, int WC>
 __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
+  constexpr int NI = WC / 32, COLS = 4 * WC;
   const int nz = (int)(a.S * a.n_ivc);
   const int id = blockIdx.x;
   const int rb = a.nrb - 1 - id / nz;
@@ -59,18 +61,18 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
   const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
   const int64_t r0 = (int64_t)rb * CTX_ROWS;
   if (r0 >= Lc) return;  // a ragged last interval has fewer row blocks
-  const int64_t e0 = (int64_t)blockIdx.y * CTX_COLS;
+  const int64_t e0 = (int64_t)blockIdx.y * COLS;
 
   __shared__ __attribute__((aligned(16))) bf16_t Ahi[CTX_ROWS * CK];
   __shared__ __attribute__((aligned(16))) bf16_t Alo[CTX_ROWS * CK];
-  __shared__ __attribute__((aligned(16))) bf16_t Bv[CTX_COLS * CK];
+  __shared__ __attribute__((aligned(16))) bf16_t Bv[COLS * CK];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int64_t b = s / a.H, h = s - b * a.H;
   const bf16_t* VT = a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp + t0;
   const int64_t pstride = a.S * a.n_iv * a.Lp * a.Lp;
   const float* P0 = a.part + (s * a.n_iv + iv) * a.Lp * a.Lp;
-  const int64_t ecol = e0 + wave * 64;  // this wave's 64 output columns
+  const int64_t ecol = e0 + wave * WC;  // this wave's WC output columns
   const bool wave_on = ecol < a.D;
   // Columns [0, kend) of the score rows r0 .. r0+63 are written by the gram
   // (zero on and above the diagonal); past kend nothing is read.
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
   const int dv = tid >> 2, kc = tid & 3;
   struct Stage {
     float4 p[2][KS];
-    uint4 v[4];
+    uint4 v[NI * 2];
   } st;
   auto load = [&](int kt) {
     const int64_t k0 = (int64_t)kt * CK;
@@ -98,7 +100,7 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st.v[i] = ldg16(VT + (e0 + dv + 64 * i) * a.Tp + k0 + kc * 8);
+    for (int i = 0; i < NI * 2; ++i) st.v[i] = ldg16(VT + (e0 + dv + 64 * i) * a.Tp + k0 + kc * 8);
   };
   auto store = [&](int kt) {
     const int64_t k0 = (int64_t)kt * CK;
@@ -124,14 +126,14 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
           make_uint2(pack_bf16x2(sv.x - hx, sv.y - hy), pack_bf16x2(sv.z - hz, sv.w - hw));
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&Bv[cofs(dv + 64 * i, kc)]) = st.v[i];
+    for (int i = 0; i < NI * 2; ++i) *reinterpret_cast<uint4*>(&Bv[cofs(dv + 64 * i, kc)]) = st.v[i];
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[2][NI];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = zero16();
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = zero16();
 
   load(0);
   for (int kt = 0; kt < nk; ++kt) {
@@ -142,19 +144,19 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
 #pragma unroll
       for (int kk = 0; kk < CK / 16; ++kk) {
         const int c = 2 * kk + (lane >> 5);
-        bf16x8 ah[2], al[2], bv[2];
+        bf16x8 ah[2], al[2], bv[NI];
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
           ah[mi] = *reinterpret_cast<const bf16x8*>(&Ahi[cofs(mi * 32 + (lane & 31), c)]);
           al[mi] = *reinterpret_cast<const bf16x8*>(&Alo[cofs(mi * 32 + (lane & 31), c)]);
         }
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-          bv[ni] = *reinterpret_cast<const bf16x8*>(&Bv[cofs(wave * 64 + ni * 32 + (lane & 31), c)]);
+        for (int ni = 0; ni < NI; ++ni)
+          bv[ni] = *reinterpret_cast<const bf16x8*>(&Bv[cofs(wave * WC + ni * 32 + (lane & 31), c)]);
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-          for (int ni = 0; ni < 2; ++ni) {
+          for (int ni = 0; ni < NI; ++ni) {
             acc[mi][ni] = mfma32(ah[mi], bv[ni], acc[mi][ni]);
             acc[mi][ni] = mfma32(al[mi], bv[ni], acc[mi][ni]);
           }
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
+    for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = r0 + mi * 32 + acc_row(lane, r);
@@ -177,16 +179,26 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
       }
 }
 
-hipError_t launch_ctx(const CtxArgs& c, int ks, hipStream_t st) {
-  const dim3 grid((unsigned)(c.nrb * c.S * c.n_ivc), (unsigned)((c.D + CTX_COLS - 1) / CTX_COLS));
+template <int WC>
+hipError_t launch_ctx_wc(const CtxArgs& c, int ks, hipStream_t st) {
+  const int cols = 4 * WC;
+  const dim3 grid((unsigned)(c.nrb * c.S * c.n_ivc), (unsigned)((c.D + cols - 1) / cols));
   switch (ks) {
-    case 1: hipLaunchKernelGGL(ctx_kernel<1>, grid, dim3(256), 0, st, c); break;
-    case 2: hipLaunchKernelGGL(ctx_kernel<2>, grid, dim3(256), 0, st, c); break;
-    case 4: hipLaunchKernelGGL(ctx_kernel<4>, grid, dim3(256), 0, st, c); break;
-    case 8: hipLaunchKernelGGL(ctx_kernel<8>, grid, dim3(256), 0, st, c); break;
+    case 1: hipLaunchKernelGGL((ctx_kernel<1, WC>), grid, dim3(256), 0, st, c); break;
+    case 2: hipLaunchKernelGGL((ctx_kernel<2, WC>), grid, dim3(256), 0, st, c); break;
+    case 4: hipLaunchKernelGGL((ctx_kernel<4, WC>), grid, dim3(256), 0, st, c); break;
+    case 8: hipLaunchKernelGGL((ctx_kernel<8, WC>), grid, dim3(256), 0, st, c); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// Measured at C2 (256 wide workgroups): narrow 24.2 us against 26.6; at C4
+// and C5 (512 and more wide workgroups) narrow is slower.
+hipError_t launch_ctx(const CtxArgs& c, int ks, hipStream_t st) {
+  const int64_t wide = c.nrb * c.S * c.n_ivc * ((c.D + CTX_COLS - 1) / CTX_COLS);
+  if (wide < 2 * (int64_t)device_cus()) return launch_ctx_wc<32>(c, ks, st);
+  return launch_ctx_wc<64>(c, ks, st);
 }
 
 // ctx[s, t0 + t, :] += sum over the rd_kr readout partials (fixed order),
