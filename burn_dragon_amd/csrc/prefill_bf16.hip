@@ -223,13 +223,12 @@ __global__ __launch_bounds__(256) void readout_add_kernel(const float* __restric
   *reinterpret_cast<float4*>(&ctx[(s * T + t0 + t) * D + d]) = v;
 }
 
-// vt[bv, d, t] = v[bv, t, d] for t < T, d < D; 0 for T <= t < Tp or D <= d < Dp.
-__global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restrict__ v,
-                                                          bf16_t* __restrict__ vt, int64_t T,
-                                                          int64_t D, int64_t Tp, int64_t Dp) {
+// vt[bv, d, t] = v[bv, t, d] for t < T, d < D; 0 for T <= t < Tp or D <= d < Dp:
+// the 32 x 32 tile (t0, d0) of slab bv.
+__device__ __forceinline__ void transpose_v_tile(const bf16_t* __restrict__ v, bf16_t* __restrict__ vt,
+                                                 int64_t T, int64_t D, int64_t Tp, int64_t Dp,
+                                                 int64_t bv, int64_t t0, int64_t d0) {
   __shared__ bf16_t tile[32][33];
-  const int64_t bv = blockIdx.z;
-  const int64_t t0 = (int64_t)blockIdx.x * 32, d0 = (int64_t)blockIdx.y * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
   for (int r = ty; r < 32; r += 8) {
     const int64_t t = t0 + r, d = d0 + tx;
@@ -242,13 +241,16 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restri
   }
 }
 
-// Packed bf16 (cos, sin) of the RoPE phase of (token, pair): low half cos.
-__global__ __launch_bounds__(256) void rope_table_bf16_kernel(const float* __restrict__ freqs,
-                                                              uint32_t* __restrict__ cs, int64_t T,
-                                                              int64_t half, int64_t pos_first,
-                                                              int fixed) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= T * half) return;
+__global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restrict__ v,
+                                                          bf16_t* __restrict__ vt, int64_t T,
+                                                          int64_t D, int64_t Tp, int64_t Dp) {
+  transpose_v_tile(v, vt, T, D, Tp, Dp, blockIdx.z, (int64_t)blockIdx.x * 32, (int64_t)blockIdx.y * 32);
+}
+
+// Packed bf16 (cos, sin) of the RoPE phase of (token, pair) i: low half cos.
+__device__ __forceinline__ void rope_table_entry(const float* __restrict__ freqs,
+                                                 uint32_t* __restrict__ cs, int64_t i, int64_t half,
+                                                 int64_t pos_first, int fixed) {
   const int64_t t = i / half;
   const int64_t k = i - t * half;
   const float p = (float)(fixed ? pos_first : pos_first + t);
@@ -257,6 +259,26 @@ __global__ __launch_bounds__(256) void rope_table_bf16_kernel(const float* __res
   // error (~1e-6) is far below the bf16 rounding of the table.
   const float fr = rope_frac(p, freqs[2 * k]);
   cs[i] = pack_bf16x2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
+}
+
+// V^T and the RoPE table in one launch (both are short and independent):
+// workgroups [0, ntr) are transpose tiles (t fastest, then d, then slab), the
+// rest 256 table entries each.
+__global__ __launch_bounds__(256) void prep_bf16_kernel(const bf16_t* __restrict__ v,
+                                                        bf16_t* __restrict__ vt, int64_t T,
+                                                        int64_t D, int64_t Tp, int64_t Dp,
+                                                        int64_t slabs, const float* __restrict__ freqs,
+                                                        uint32_t* __restrict__ cs, int64_t half,
+                                                        int64_t pos_first, int fixed) {
+  const int64_t gt = Tp / 32, gd = Dp / 32, ntr = gt * gd * slabs;
+  const int64_t id = blockIdx.x;
+  if (id < ntr) {
+    const int64_t tile = id % (gt * gd);
+    transpose_v_tile(v, vt, T, D, Tp, Dp, id / (gt * gd), (tile % gt) * 32, (tile / gt) * 32);
+    return;
+  }
+  const int64_t i = (id - ntr) * 256 + threadIdx.x;
+  if (i < T * half) rope_table_entry(freqs, cs, i, half, pos_first, fixed);
 }
 
 // q[s, t, :] = rope(x[s, t, :]) in bf16: phase frac(p f) in the reference's
@@ -402,9 +424,16 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   }
   const bool rope = a.freqs != nullptr && !prerot;
 
-  hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, 32), cdiv(Dp, 32), (unsigned)(a.B * a.Hv)),
-                     dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
   uint64_t n_launch = 1;
+  if (rope) {
+    const int64_t ntr = (Tp / 32) * (Dp / 32) * a.B * a.Hv;
+    hipLaunchKernelGGL(prep_bf16_kernel, dim3((unsigned)ntr + cdiv(a.T * half, 256)), dim3(256), 0, st,
+                       a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp, a.B * a.Hv, a.freqs, (uint32_t*)cs, half,
+                       a.pos0, a.fixed);
+  } else {
+    hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, 32), cdiv(Dp, 32), (unsigned)(a.B * a.Hv)),
+                       dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
+  }
   BDH_HIP_TRY(hipGetLastError());
   if (prerot) {
     // Launches of at most 2^22 workgroups (2^30 work-items) each.
@@ -417,11 +446,6 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
       BDH_HIP_TRY(hipGetLastError());
       ++n_launch;
     }
-  } else if (rope) {
-    hipLaunchKernelGGL(rope_table_bf16_kernel, dim3(cdiv(a.T * half, 256)), dim3(256), 0, st,
-                       a.freqs, (uint32_t*)cs, a.T, half, a.pos0, a.fixed);
-    BDH_HIP_TRY(hipGetLastError());
-    ++n_launch;
   }
 
   PrefillArgs p{};
