@@ -144,6 +144,7 @@ struct PrefillArgs {
   float* rho_out;       // [S, N, D]
   int64_t st_t0, st_Lc, Tp, Dp;  // Tp >= st_t0 + st_Lc rounded up to 64
   int state_units;      // prefill_state_units(S, N, D), or 0
+  int rho_stream;       // rho_out is the caller's final state (streaming stores)
   // readout units: partial (Q * d^r) rho_iv for the interval
   // [rd_t0, rd_t0 + rd_Lc), rho_iv the state at its start
   const float* rd_rho;  // [S, N, D]

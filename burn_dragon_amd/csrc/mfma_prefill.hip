@@ -216,7 +216,14 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
       v.z += pv.z * carry;
       v.w += pv.w * carry;
     }
-    *reinterpret_cast<float4*>(&a.rho_out[idx]) = v;
+    // The caller's final state is not read again here: a streaming store
+    // keeps the x rows that the gram tiles share in the caches (C2: 0.390 ->
+    // 0.369 ms).  A state between intervals is read by the next launch and
+    // stays cached.
+    if (a.rho_stream)
+      __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, reinterpret_cast<floatx4*>(&a.rho_out[idx]));
+    else
+      *reinterpret_cast<float4*>(&a.rho_out[idx]) = v;
   });
 }
 

@@ -482,6 +482,7 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     p.st_t0 = t0;
     p.st_Lc = Lc;
     p.state_units = (a.state && !in_place) ? state_units : 0;
+    p.rho_stream = next == a.rho_out;
     BDH_HIP_TRY(launch_prefill_mfma(p, rope, st));
     ++n_launch;
     if (a.state && in_place) {
