@@ -182,7 +182,8 @@ __global__ __launch_bounds__(DR_THREADS) void decode_kernel(DecodeKernelArgs p) 
             nr.w = fmaf(rv[u], vv.w, row[u].w);
           }
           if (k < seg_total && cv) {
-            if (VEC4) *reinterpret_cast<float4*>(ptr[u]) = nr;
+            if (VEC4)  // streaming: a step does not read its rows again
+              __builtin_nontemporal_store(floatx4{nr.x, nr.y, nr.z, nr.w}, reinterpret_cast<floatx4*>(ptr[u]));
             else *ptr[u] = nr.x;
           }
         }
