@@ -38,9 +38,9 @@ SEED = 20260729
 # profiles/prefill_c2_traffic.txt, profiles/decode_c3_traffic.txt,
 # profiles/long_prefill_c4_traffic.txt.  Counters cannot run inside this
 # process, so the figures are recorded here; they change when the kernels do.
-TRAFFIC_PREFILL_C2 = 1468.3e6   # prefill pass (transpose, table, prefill launch, ctx)
-TRAFFIC_DECODE_C3 = 428.0e6     # one decode_kernel launch
-TRAFFIC_LONG_C4 = 5635.5e6      # one C4 prefill call (rotation, 16 prefill launches, ctx, 15 adds)
+TRAFFIC_PREFILL_C2 = 1403.2e6   # prefill pass (transpose, table, prefill launch, ctx)
+TRAFFIC_DECODE_C3 = 428.1e6     # one decode_kernel launch
+TRAFFIC_LONG_C4 = 5626.7e6      # one C4 prefill call (rotation, 16 prefill launches, ctx, 15 adds)
 
 
 def parse():
