@@ -38,9 +38,9 @@ SEED = 20260729
 # profiles/prefill_c2_traffic.txt, profiles/decode_c3_traffic.txt,
 # profiles/long_prefill_c4_traffic.txt.  Counters cannot run inside this
 # process, so the figures are recorded here; they change when the kernels do.
-TRAFFIC_PREFILL_C2 = 1403.2e6   # prefill pass (transpose, table, prefill launch, ctx)
+TRAFFIC_PREFILL_C2 = 1327.5e6   # one prefill_mfma_kernel launch (the pass: 1403.2e6)
 TRAFFIC_DECODE_C3 = 428.1e6     # one decode_kernel launch
-TRAFFIC_LONG_C4 = 5626.7e6      # one C4 prefill call (rotation, 16 prefill launches, ctx, 15 adds)
+TRAFFIC_LONG_C4 = 3861.0e6      # the 16 prefill_mfma_kernel launches of one C4 call (the call: 5626.7e6)
 
 
 def parse():
@@ -78,6 +78,29 @@ def lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho):
         raise RuntimeError(f"prefill failed: {_lib.last_error()}")
 
 
+def kernel_times(lib, kind):
+    """(summed ms, launches) of the dominant kernel `kind` recorded since
+    bdh_profile_kernel_timing(1): HIP events on the launch stream around each
+    of its launches."""
+    from burn_dragon_amd import _lib
+    ms, n = ctypes.c_double(), ctypes.c_int64()
+    if lib.bdh_profile_kernel_get(kind, ctypes.byref(ms), ctypes.byref(n)) != 0:
+        raise RuntimeError(f"kernel timing failed: {_lib.last_error()}")
+    return ms.value, n.value
+
+
+def timed_kernel(torch, lib, kind, steps, call):
+    """Run `call` `steps` times with kernel timing on; returns (ms per call of
+    the kernel, launches per call)."""
+    lib.bdh_profile_kernel_timing(1)
+    for _ in range(steps):
+        call()
+    torch.cuda.synchronize()
+    ms, n = kernel_times(lib, kind)
+    lib.bdh_profile_kernel_timing(0)
+    return ms / steps, n / steps
+
+
 def bench_prefill(torch, args):
     from burn_dragon_amd import _lib
     B, H, T, N, D, C = 8, 4, 512, 8192, 256, 128
@@ -106,18 +129,27 @@ def bench_prefill(torch, args):
     ev_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / args.steps
     flop = B * H * T * (4 * N * D + (C - 1) * (N + D))
     ms = wall * 1e3 / args.steps
-    achieved = flop / (ev_ms * 1e-3) / 1e12
+    pass_tflops = flop / (ev_ms * 1e-3) / 1e12
+    # The dominant kernel, timed in its own loop: prefill_mfma_kernel does all
+    # of the pass's algorithmic work except the intra-chunk S.V (C-1)D per
+    # token, which is the context kernel's.
+    k_ms, k_n = timed_kernel(torch, lib, _lib.BDH_KERNEL_PREFILL, args.steps,
+                             lambda: lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho))
+    k_flop = B * H * T * (4 * N * D + (C - 1) * N)
+    achieved = k_flop / k_n / (k_ms / k_n * 1e-3) / 1e12
     print(f"[prefill] {ms:.3f} ms/step wall, {ev_ms:.3f} ms/step events, "
-          f"{B * T / (ms * 1e-3) / 1e6:.2f} M tok/s, {achieved:.1f} TFLOP/s", flush=True)
+          f"{B * T / (ms * 1e-3) / 1e6:.2f} M tok/s, {pass_tflops:.1f} TFLOP/s per pass; "
+          f"prefill_mfma_kernel {k_ms / k_n * 1e3:.1f} us, {achieved:.1f} TFLOP/s", flush=True)
     return {
         "ms_per_step": ms, "event_ms": ev_ms, "tokens_per_s": B * T / (ms * 1e-3),
         "flop": flop,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": TRAFFIC_PREFILL_C2,
-                     "kernel": "prefill pass: prefill_mfma_kernel (gram + state units) + ctx_kernel "
-                               "(+ rope table, V transpose), timed as one unit",
-                     "flop_per_launch": flop},
+                     "traffic": TRAFFIC_PREFILL_C2, "kernel": "prefill_mfma_kernel",
+                     "kernel_avg_us": round(k_ms / k_n * 1e3, 2), "flop_per_launch": k_flop / k_n,
+                     "pass": {"kernels": "prep_bf16_kernel + prefill_mfma_kernel + ctx_kernel",
+                              "event_ms": round(ev_ms, 4), "tflops": round(pass_tflops, 2),
+                              "flop": flop, "traffic": 1403.2e6}},
         "shape": {"B": B, "nh": H, "T": T, "N": N, "D": D, "chunk": C},
     }
 
@@ -148,16 +180,25 @@ def bench_long(torch, args):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     flop = B * H * T * (4 * N * D + (C - 1) * (N + D))
-    achieved = flop / (ms * 1e-3) / 1e12
+    call_tflops = flop / (ms * 1e-3) / 1e12
+    # The dominant kernel: its 16 launches per call, summed.
+    k_ms, k_n = timed_kernel(torch, lib, _lib.BDH_KERNEL_PREFILL, steps,
+                             lambda: lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho))
+    k_flop = B * H * T * (4 * N * D + (C - 1) * N)
+    achieved = k_flop / (k_ms * 1e-3) / 1e12
     print(f"[long] {ms:.3f} ms/prefill, {B * T / (ms * 1e-3) / 1e6:.2f} M tok/s, "
-          f"{achieved:.1f} TFLOP/s", flush=True)
+          f"{call_tflops:.1f} TFLOP/s per call; prefill_mfma_kernel {k_n:.0f} launches, "
+          f"{k_ms:.3f} ms, {achieved:.1f} TFLOP/s", flush=True)
     return {"metric": "C4 long-context prefill tokens/s per BDH layer", "value": B * T / (ms * 1e-3),
             "unit": "tokens/s", "ms_per_prefill": ms, "steps": steps,
             "config": {"workload": "C4 long prefill, one BDH layer: B1 nh4 T8192 N8192 D256, "
                                    "chunk 256, bf16 in / fp32 acc, RoPE fused"},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                         "traffic": TRAFFIC_LONG_C4, "flop_per_launch": flop}}
+                         "traffic": TRAFFIC_LONG_C4,
+                         "kernel": f"prefill_mfma_kernel, {k_n:.0f} launches per call (summed)",
+                         "kernel_ms_per_call": round(k_ms, 4), "flop_per_call": k_flop,
+                         "call": {"tflops": round(call_tflops, 2), "flop": flop, "traffic": 5626.7e6}}}
 
 
 def bench_decode(torch, args):
@@ -219,12 +260,16 @@ def bench_decode(torch, args):
     S = B * H
     bytes_total = K * S * (4 * N + 4 * D + 4 * D) + active * 2 * 4 * D
     bytes_per_step = bytes_total / K
-    achieved = bytes_per_step / (ev_ms * 1e-3) / 1e9
+    # The kernel alone, timed in its own loop over the same inputs and
+    # positions (the same active rows, so the same algorithmic bytes).
+    it = iter(range(W, W + K))
+    k_ms, k_n = timed_kernel(torch, lib, _lib.BDH_KERNEL_DECODE, K, lambda: step(next(it)))
+    achieved = bytes_per_step / (k_ms / k_n * 1e-3) / 1e9
     ms = wall * 1e3 / K
     frac_active = active / (K * S * N)
     print(f"[decode] {ms:.4f} ms/step wall, {ev_ms:.4f} ms/step events, "
-          f"{B / (ms * 1e-3) / 1e6:.3f} M tok/s, {achieved:.0f} GB/s, active {frac_active:.4f}",
-          flush=True)
+          f"{B / (ms * 1e-3) / 1e6:.3f} M tok/s, decode_kernel {k_ms / k_n * 1e3:.1f} us, "
+          f"{achieved:.0f} GB/s, active {frac_active:.4f}", flush=True)
     del xs, vs, rho
     return {
         "value": B / (ms * 1e-3), "unit": "tokens/s", "steps": K, "warmup": W,
@@ -234,7 +279,8 @@ def bench_decode(torch, args):
         "active_fraction": round(frac_active, 5),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_DECODE_C3,
-                     "kernel": "decode_kernel", "bytes_per_launch": round(bytes_per_step)},
+                     "kernel": "decode_kernel", "kernel_avg_us": round(k_ms / k_n * 1e3, 2),
+                     "bytes_per_launch": round(bytes_per_step)},
     }
 
 

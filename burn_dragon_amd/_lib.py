@@ -21,6 +21,7 @@ BDH_EHIP = -2
 BDH_F32 = 0
 BDH_BF16 = 1
 
+BDH_KERNEL_PREFILL, BDH_KERNEL_DECODE = 0, 1
 BDH_ROPE_SEQUENTIAL = 0
 BDH_ROPE_FIXED = 1
 
@@ -72,6 +73,9 @@ SIGNATURES = {
     "bdh_profile_enable": (None, [_i32]),
     "bdh_profile_reset": (None, []),
     "bdh_profile_get": (None, [ctypes.POINTER(BdhProfileSnapshot)]),
+    "bdh_profile_kernel_timing": (_i32, [_i32]),
+    "bdh_profile_kernel_get": (_i32, [_i32, ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_int64)]),
     "bdh_last_error": (ctypes.c_char_p, []),
     "bdh_version": (ctypes.c_char_p, []),
 }

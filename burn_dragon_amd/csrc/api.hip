@@ -4,6 +4,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <atomic>
 #include <chrono>
 #include <map>
 #include <mutex>
@@ -130,6 +131,56 @@ struct ProfScope {
   }
 };
 }  // namespace
+
+// ----------------------------------------------------------- kernel timing --
+namespace {
+struct KTimeRec {
+  hipEvent_t start, stop;
+  int kind;
+};
+std::mutex g_kt_mu;
+std::atomic<bool> g_kt_on{false};
+std::vector<KTimeRec> g_kt_recs;
+std::vector<hipEvent_t> g_kt_pool;
+
+hipEvent_t kt_event() {
+  if (!g_kt_pool.empty()) {
+    hipEvent_t e = g_kt_pool.back();
+    g_kt_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+void kt_clear() {
+  for (auto& r : g_kt_recs) {
+    g_kt_pool.push_back(r.start);
+    g_kt_pool.push_back(r.stop);
+  }
+  g_kt_recs.clear();
+}
+}  // namespace
+
+int ktime_begin(int kind, hipStream_t st) {
+  if (!g_kt_on) return -1;
+  std::lock_guard<std::mutex> lock(g_kt_mu);
+  KTimeRec r{kt_event(), kt_event(), kind};
+  if (!r.start || !r.stop || hipEventRecord(r.start, st) != hipSuccess) {
+    if (r.start) g_kt_pool.push_back(r.start);
+    if (r.stop) g_kt_pool.push_back(r.stop);
+    return -1;
+  }
+  g_kt_recs.push_back(r);
+  return (int)g_kt_recs.size() - 1;
+}
+
+void ktime_end(int handle, hipStream_t st) {
+  if (handle < 0) return;
+  std::lock_guard<std::mutex> lock(g_kt_mu);
+  if (handle < (int)g_kt_recs.size()) (void)hipEventRecord(g_kt_recs[handle].stop, st);
+}
 
 }  // namespace bdh
 
@@ -463,6 +514,32 @@ void bdh_profile_get(bdh_profile_snapshot* out) {
   if (!out) return;
   std::lock_guard<std::mutex> lock(g_prof_mu);
   *out = g_prof;
+}
+
+bdh_status bdh_profile_kernel_timing(int32_t enabled) {
+  std::lock_guard<std::mutex> lock(g_kt_mu);
+  for (auto& r : g_kt_recs) BDH_HIP_TRY(hipEventSynchronize(r.stop));
+  kt_clear();
+  g_kt_on = enabled != 0;
+  return BDH_OK;
+}
+
+bdh_status bdh_profile_kernel_get(int32_t kind, double* total_ms, int64_t* launches) {
+  if (!total_ms || !launches) return fail(BDH_EINVAL, "null output pointer");
+  std::lock_guard<std::mutex> lock(g_kt_mu);
+  double sum = 0.0;
+  int64_t n = 0;
+  for (auto& r : g_kt_recs) {
+    if (r.kind != kind) continue;
+    BDH_HIP_TRY(hipEventSynchronize(r.stop));
+    float ms = 0.0f;
+    BDH_HIP_TRY(hipEventElapsedTime(&ms, r.start, r.stop));
+    sum += ms;
+    ++n;
+  }
+  *total_ms = sum;
+  *launches = n;
+  return BDH_OK;
 }
 
 const char* bdh_last_error(void) { return g_last_error.c_str(); }

@@ -48,6 +48,12 @@ bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = fals
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus();
 
+// Kernel timing (bdh_profile_kernel_timing): ktime_begin records a start
+// event on `st` and returns a handle (-1 when timing is off); ktime_end
+// records the matching stop event.
+int ktime_begin(int kind, hipStream_t st);
+void ktime_end(int handle, hipStream_t st);
+
 // Device copy of the RoPE frequency table for (latent, theta), cached.
 bdh_status rope_freqs_device(int64_t latent, float theta, const float** out);
 // Host computation of the same table (attention.rs:552-576).

@@ -277,6 +277,7 @@ bdh_status run_decode(const DecodeArgs& a, hipStream_t st, uint64_t* launches) {
   }
   const dim3 grid((unsigned)(S * G));
   const bool vec4 = (a.D % 4) == 0;
+  const int kt = ktime_begin(BDH_KERNEL_DECODE, st);
   if (a.freqs) {
     if (vec4) hipLaunchKernelGGL((decode_kernel<true, true>), grid, dim3(DR_THREADS), 0, st, p);
     else hipLaunchKernelGGL((decode_kernel<true, false>), grid, dim3(DR_THREADS), 0, st, p);
@@ -284,6 +285,7 @@ bdh_status run_decode(const DecodeArgs& a, hipStream_t st, uint64_t* launches) {
     if (vec4) hipLaunchKernelGGL((decode_kernel<false, true>), grid, dim3(DR_THREADS), 0, st, p);
     else hipLaunchKernelGGL((decode_kernel<false, false>), grid, dim3(DR_THREADS), 0, st, p);
   }
+  ktime_end(kt, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "decode_kernel launch");
   if (launches) *launches += 1;

@@ -483,14 +483,18 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     p.st_Lc = Lc;
     p.state_units = (a.state && !in_place) ? state_units : 0;
     p.rho_stream = next == a.rho_out;
+    int kt = ktime_begin(BDH_KERNEL_PREFILL, st);
     BDH_HIP_TRY(launch_prefill_mfma(p, rope, st));
+    ktime_end(kt, st);
     ++n_launch;
     if (a.state && in_place) {
       PrefillArgs q = p;
       q.gram_ids = 0;
       q.rd_units = 0;
       q.state_units = state_units;
+      kt = ktime_begin(BDH_KERNEL_PREFILL, st);
       BDH_HIP_TRY(launch_prefill_mfma(q, rope, st));
+      ktime_end(kt, st);
       ++n_launch;
     }
     if (iv == 0) {

@@ -205,6 +205,18 @@ void bdh_profile_enable(int32_t enabled);
 void bdh_profile_reset(void);
 void bdh_profile_get(bdh_profile_snapshot* out);
 
+/* Device time of the dominant kernel of each path, from HIP events recorded
+ * on the launch stream right before and after each of its launches.  No
+ * counterpart in the reference: a measurement hook for benchmarks (the
+ * roofline of one kernel).  Enabling (or disabling) clears what was
+ * recorded.  kind: BDH_KERNEL_PREFILL = prefill_mfma_kernel (gram, readout
+ * and state units), BDH_KERNEL_DECODE = decode_kernel.  bdh_profile_kernel_get
+ * waits for the recorded launches and returns their summed milliseconds and
+ * their count. */
+typedef enum { BDH_KERNEL_PREFILL = 0, BDH_KERNEL_DECODE = 1 } bdh_kernel_kind;
+bdh_status bdh_profile_kernel_timing(int32_t enabled);
+bdh_status bdh_profile_kernel_get(int32_t kind, double* total_ms, int64_t* launches);
+
 /* Thread-local message of the last non-OK status of this thread. */
 const char* bdh_last_error(void);
 

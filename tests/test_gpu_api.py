@@ -91,3 +91,35 @@ def test_memory_stays_bounded_across_repeated_calls():
     torch.cuda.synchronize()
     assert torch.cuda.memory_allocated() - base <= 64 * 1024 * 1024
     assert torch.isfinite(rho).all()
+
+
+def test_kernel_timing_records_the_dominant_kernels():
+    # bdh_profile_kernel_timing / _get: events around prefill_mfma_kernel and
+    # decode_kernel launches; nothing recorded while off.
+    import ctypes
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    from burn_dragon_amd import _lib
+    lib = _lib.load()
+
+    def got(kind):
+        ms, n = ctypes.c_double(), ctypes.c_int64()
+        assert lib.bdh_profile_kernel_get(kind, ctypes.byref(ms), ctypes.byref(n)) == _lib.BDH_OK
+        return ms.value, n.value
+
+    x = torch.relu(torch.randn(1, 2, 256, 256, device="cuda") - 1.0).to(torch.bfloat16)
+    v = (torch.randn(1, 1, 256, 64, device="cuda") / 16).to(torch.bfloat16)
+    xd = torch.relu(torch.randn(1, 2, 256, device="cuda") - 1.0)
+    vd = torch.randn(1, 1, 64, device="cuda")
+    announce("api kernel timing")
+    assert lib.bdh_profile_kernel_timing(1) == _lib.BDH_OK
+    out = bd.try_fused_recurrent_attention_rope(x, v, position=0)
+    bd.decode_step(xd, vd, out.rho, position=256)
+    torch.cuda.synchronize()
+    pm, pn = got(_lib.BDH_KERNEL_PREFILL)
+    dm, dn = got(_lib.BDH_KERNEL_DECODE)
+    assert pn == 1 and pm > 0 and dn == 1 and dm > 0
+    assert lib.bdh_profile_kernel_timing(0) == _lib.BDH_OK
+    bd.try_fused_recurrent_attention_rope(x, v, position=0)
+    torch.cuda.synchronize()
+    assert got(_lib.BDH_KERNEL_PREFILL) == (0.0, 0)
