@@ -3,7 +3,8 @@ recurrent linear-attention forward path (chunked bf16-MFMA prefill with fused
 RoPE, sparse bandwidth-bound decode), behind the reference's custom-op
 surface.  The compute lives in libbdh_hip.so (C ABI: include/bdh_hip.h)."""
 from .recurrent import (CompiledRecurrentAttentionPlan, KernelProfileSnapshot,  # noqa: F401
-                        RecurrentAttentionOutput, RecurrentProfileSnapshot,
+                        RecurrentAttentionOutput, RecurrentProfileSnapshot, alibi_decay,
+                        default_alibi_slopes,
                         recurrent_profile_enable, recurrent_profile_reset,
                         recurrent_profile_snapshot, supports_backend,
                         supports_recurrent_backend, try_fused_recurrent_attention,

@@ -54,6 +54,22 @@ class CompiledRecurrentAttentionPlan:
         return p if _lib.check(st) else None
 
 
+def default_alibi_slopes(n_head: int) -> list:
+    """linear_attention::default_alibi_slopes (kernel/linear_attention.rs:149-160):
+    slope_h = 1 / 2^(h / n_head), in f32."""
+    import numpy as np
+    return [float(np.float32(1.0) / np.power(np.float32(2.0), np.float32(h) / np.float32(n_head)))
+            for h in range(n_head)]
+
+
+def alibi_decay(slopes) -> "torch.Tensor":
+    """Per-head decay exp(-slope) of the ALiBi variant (attention.rs:201-208), f32 on
+    the CPU; pass it (on the device) as ``decay`` with ``rho`` the layer's state and
+    no RoPE (the ALiBi arm's frequencies are 0, attention.rs:569)."""
+    import numpy as np
+    return torch.from_numpy(np.exp(-np.asarray(slopes, np.float32)).astype(np.float32))
+
+
 def supports_backend() -> bool:
     """recurrent.rs:151-173 (exported as supports_recurrent_backend)."""
     if not torch.cuda.is_available():

@@ -148,6 +148,28 @@ def test_bf16_rope_fixed_mode(oracle, T):
     assert rel_l2(ctx, cref) <= TOL_BF16 and rel_l2(rho, rref) <= TOL_BF16
 
 
+def test_bf16_alibi_dense_score_short_context(oracle):
+    # DenseScoreShortContext with ALiBi (sequence_dispatch.rs:137-198): the
+    # fused dense context + initial_context(rho0) + final_rho of the
+    # reference are one call here, with decay = exp(-slope) (default slopes),
+    # rho = the layer's state and no rotation (the ALiBi arm's frequencies
+    # are zero, attention.rs:569).  Checked against the dense-score closed
+    # form (linear.rs:221-364).
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(57)
+    B, H, T, N, D = 2, 4, 300, 512, 64
+    x, v, rho0 = _bf16_case(rng, B, H, 1, T, N, D, True)
+    dec = bd.alibi_decay(bd.default_alibi_slopes(H)).numpy()
+    xb, vb = oracle.round_bf16(x), oracle.round_bf16(v)
+    announce("bf16 alibi dense-score", B, H, T, N, D)
+    ctx, rho = _run(torch, bd, xb, vb, rho0, dec, dtype=torch.bfloat16)
+    cref, rref = oracle.dense_score_f64(xb, vb, rho0, dec)
+    e_ctx, e_rho = rel_l2(ctx, cref), rel_l2(rho, rref)
+    print(f"rel-L2 ctx {e_ctx:.2e} rho {e_rho:.2e}")
+    assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
+
+
 def test_bf16_prerotated_query(oracle):
     torch = need_gpu()
     import burn_dragon_amd as bd

@@ -259,3 +259,16 @@ def test_checks_catch_planted_mistakes(oracle):
     x = np.array([[[0.0, 1.0]]], np.float32)
     good = oracle.rope_rotate(x, pos0=1)
     assert good[0, 0, 0] < 0  # -sin(phi) for phi in (0, pi)
+
+
+def test_alibi_helpers_match_reference_formulas():
+    # default_alibi_slopes (kernel/linear_attention.rs:149-160): 1 / 2^(h/H);
+    # decay = exp(-slope) (attention.rs:201-208), e.g. the cached-decay test's
+    # slopes [0.25, 0.75] (linear.rs:535-587).
+    import math
+    from burn_dragon_amd.recurrent import alibi_decay, default_alibi_slopes
+    s4 = default_alibi_slopes(4)
+    assert [round(v, 6) for v in s4] == [round(2.0 ** (-h / 4), 6) for h in range(4)]
+    assert s4[0] == 1.0 and default_alibi_slopes(0) == []
+    d = alibi_decay([0.25, 0.75]).numpy()
+    assert abs(d[0] - math.exp(-0.25)) < 1e-7 and abs(d[1] - math.exp(-0.75)) < 1e-7
