@@ -35,8 +35,10 @@ using namespace mfma;
 
 // ---------------------------------------------------------------------------
 // gram unit: rows ri .. ri+255 (A) x columns rj .. rj+127 (B) of interval iv,
-// N range [kb, ke) in BK steps.
-template <bool ROPE, bool DECAY, bool WHOLE>
+// N range [kb, ke) in BK steps.  PAIR: two diagonal 128 x 128 blocks, rows
+// and columns ri .. ri+127 (waves 0, 1) and rj .. rj+127 (waves 2, 3; rj < 0:
+// none), each the lower part of a 256-row block's last 128-column tile.
+template <bool ROPE, bool DECAY, bool WHOLE, bool PAIR = false>
 __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int64_t s, int kp,
                                           int64_t iv, int64_t ri, int64_t rj) {
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
@@ -58,8 +60,9 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   // 128) takes its B operand from the A rows already in LDS: groups 4 and 5
   // load nothing.  The row offset is a multiple of 8, so a row's swizzle is
   // the same seen from either base.
-  const bool inner = rj >= ri && rj + T256 / 2 <= ri + T256;
+  const bool inner = PAIR || (rj >= ri && rj + T256 / 2 <= ri + T256);
   const int groups = inner ? 4 : 6;
+  const int64_t rj2 = PAIR ? (rj < 0 ? ri : rj) : rj;  // second block (a pair's absent one re-reads the first)
   const int kc = tid & 3, rb = tid >> 2;
   const uint32_t lane_off = (uint32_t)(rb * rowb + kc * 16);
   struct Stage {
@@ -70,7 +73,8 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
 #pragma unroll
     for (int g = 0; g < 6; ++g) {
       if (g >= groups) break;
-      const int64_t r0 = (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
+      const int64_t r0 = PAIR ? (g < 2 ? ri + 64 * g : rj2 + 64 * (g - 2))
+                              : (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
       if (WHOLE) {
         const int64_t o = r0 * rowb + kofs;
         st.xr[g] = ldg16_off(X + o, lane_off);
@@ -96,8 +100,11 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   zero_acc(acc);
   // Waves whose 64 rows end at or before the tile's first column compute
   // nothing that is kept; nor do waves starting past a ragged interval.
-  const bool active = ri + 64 * w + 64 > rj + 1 && ri + 64 * w < Lc;
-  const int brow = inner ? (int)(rj - ri) : T256;  // LDS row of the first B row
+  // Each wave's rows start at wr0 and its columns at wc0.
+  const int64_t wc0 = PAIR ? (w < 2 ? ri : rj2) : rj;
+  const int64_t wr0 = PAIR ? wc0 + 64 * (w & 1) : ri + 64 * w;
+  const bool active = PAIR ? (wr0 < Lc && (w < 2 || rj >= 0)) : (wr0 + 64 > rj + 1 && wr0 < Lc);
+  const int brow = PAIR ? 128 * (w >> 1) : inner ? (int)(rj - ri) : T256;  // LDS row of the first B row
   run_steps(kb, ke, load, store, [&](int buf) {
     if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF, lane, 64 * w, brow, acc);
   });
@@ -108,7 +115,7 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   const float l2d = DECAY ? log2f(a.decay[s % a.H]) : 0.0f;
   float* P = a.part + (((int64_t)kp * a.S + s) * a.n_iv + iv) * a.Lp * a.Lp;
   epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
-    const int64_t ti = ri + 64 * w + row, tj = rj + col;
+    const int64_t ti = wr0 + row, tj = wc0 + col;
     if (!active || ti >= Lc) return;
     float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -315,15 +322,21 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
 }
 
 // ---------------------------------------------------------------------------
-// Gram tiles of one interval: 256-row block rb (of nb) x 128-column block cb,
-// for every cb < 2 (rb + 1); tile u enumerates them row block by row block.
-// Gram ids: blocks of 8 groups; inside a block, id = tile * 8 + (group & 7),
-// so the tiles of one group (which read the same x rows) have ids congruent
+// Gram units of one interval.  Units u < nb^2 are the tiles of 256-row block
+// rbk (of nb) x 128-column block cbk for cbk <= 2 rbk, row block by row
+// block.  The block's last column tile (cbk = 2 rbk + 1) has work only in its
+// lower 128 rows, a diagonal 128 x 128 block; those blocks go two to a unit
+// (rows 2j and 2j + 1), units nb^2 .. nb^2 + ceil(nb / 2) - 1, so that a
+// group's units carry about equal work.
+// Gram ids: blocks of 8 groups; inside a block, id = unit * 8 + (group & 7),
+// so the units of one group (which read the same x rows) have ids congruent
 // mod 8 and run on one XCD (the dispatcher sends id i to XCD i % 8).
+__device__ __forceinline__ int units_per_group(int nb) { return nb * nb + (nb + 1) / 2; }
+
 __device__ __forceinline__ void tile_of(int u, int& rbk, int& cbk) {
   rbk = 0;
-  while ((rbk + 1) * (rbk + 2) <= u) ++rbk;
-  cbk = u - rbk * (rbk + 1);
+  while ((rbk + 1) * (rbk + 1) <= u) ++rbk;
+  cbk = u - rbk * rbk;
 }
 
 template <bool ROPE, bool DECAY>
@@ -331,7 +344,7 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[2 * BUF];
   const int id = blockIdx.x;
   if (id < a.gram_ids) {
-    const int tpg = a.nb * (a.nb + 1);
+    const int tpg = units_per_group(a.nb);
     const int blk = id / (8 * tpg), rem = id - blk * 8 * tpg;
     const int u = rem >> 3;
     const int g = blk * 8 + (rem & 7);
@@ -340,10 +353,23 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
     const int q = (int)(g / a.n_iv);
     const int kp = q % a.ks;
     const int64_t s = q / a.ks;
-    int rbk, cbk;
-    tile_of(u, rbk, cbk);
     const int64_t t0 = iv * a.L;
     const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
+    if (u >= a.nb * a.nb) {
+      // Pair of diagonal blocks of row blocks 2j and 2j + 1.
+      const int j = u - a.nb * a.nb;
+      const int64_t ra = (int64_t)(2 * j) * T256 + T256 / 2;
+      int64_t rb = (int64_t)(2 * j + 1) * T256 + T256 / 2;
+      if (ra >= Lc) return;  // past a ragged last interval: never read
+      if (2 * j + 1 >= a.nb || rb >= Lc) rb = -1;
+      if (ra + T256 / 2 <= Lc && (rb < 0 || rb + T256 / 2 <= Lc))
+        gram_unit<ROPE, DECAY, true, true>(a, lds, s, kp, iv, ra, rb);
+      else
+        gram_unit<ROPE, DECAY, false, true>(a, lds, s, kp, iv, ra, rb);
+      return;
+    }
+    int rbk, cbk;
+    tile_of(u, rbk, cbk);
     const int64_t ri = (int64_t)rbk * T256, rj = (int64_t)cbk * (T256 / 2);
     if (ri >= Lc || rj >= Lc) return;  // tile past a ragged last interval: never read
     if (ri + T256 <= Lc) gram_unit<ROPE, DECAY, true>(a, lds, s, kp, iv, ri, rj);
@@ -379,7 +405,7 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
 }  // namespace
 
 int prefill_gram_ids(int groups, int nb) {
-  const int tpg = nb * (nb + 1);
+  const int tpg = nb * nb + (nb + 1) / 2;
   return ((groups + 7) / 8) * 8 * tpg;
 }
 
