@@ -44,6 +44,9 @@ enum ScratchSlot {
   SLOT_COUNT
 };
 bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);
+// Number of (re)allocations of a slot on the current device: contents kept
+// across calls are valid only while it is unchanged.
+uint64_t scratch_epoch(int slot);
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus();

@@ -18,6 +18,9 @@
 // RoPE is applied to Q tiles between HBM and LDS from a packed bf16
 // (cos, sin) table of the call's (token, pair) phases; rotated queries are
 // never written to memory.
+#include <map>
+#include <mutex>
+
 #include "bdh_bf16.h"
 
 namespace bdh {
@@ -316,6 +319,34 @@ __global__ __launch_bounds__(256) void rope_rotate_bf16_kernel(const bf16_t* __r
 
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
+// The RoPE table depends only on the positions and the frequencies: a call
+// whose key matches the table last built in the device's table buffer reuses
+// it (prefills of new sequences all start at position 0).
+struct TableKey {
+  const void* buf;
+  uint64_t epoch;  // of the table's scratch slot: a reallocation invalidates
+  const float* freqs;
+  int64_t T, half, pos0;
+  int fixed;
+  bool operator==(const TableKey& o) const {
+    return buf == o.buf && epoch == o.epoch && freqs == o.freqs && T == o.T && half == o.half &&
+           pos0 == o.pos0 && fixed == o.fixed;
+  }
+};
+std::mutex g_table_mu;
+std::map<int, TableKey> g_table;
+
+bool table_built(int dev, const TableKey& k) {
+  std::lock_guard<std::mutex> lock(g_table_mu);
+  auto it = g_table.find(dev);
+  return it != g_table.end() && it->second == k;
+}
+
+void table_record(int dev, const TableKey& k) {
+  std::lock_guard<std::mutex> lock(g_table_mu);
+  g_table[dev] = k;
+}
+
 }  // namespace
 
 bool bf16_shape_supported(int64_t N, int64_t D, const char** why) {
@@ -425,11 +456,16 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   const bool rope = a.freqs != nullptr && !prerot;
 
   uint64_t n_launch = 1;
-  if (rope) {
+  int dev = 0;
+  BDH_HIP_TRY(hipGetDevice(&dev));
+  const TableKey tkey{cs, scratch_epoch(SLOT_ROPE_TABLE), a.freqs, a.T, half, a.pos0, a.fixed};
+  if (rope && !table_built(dev, tkey)) {
     const int64_t ntr = (Tp / 32) * (Dp / 32) * a.B * a.Hv;
     hipLaunchKernelGGL(prep_bf16_kernel, dim3((unsigned)ntr + cdiv(a.T * half, 256)), dim3(256), 0, st,
                        a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp, a.B * a.Hv, a.freqs, (uint32_t*)cs, half,
                        a.pos0, a.fixed);
+    BDH_HIP_TRY(hipGetLastError());
+    table_record(dev, tkey);
   } else {
     hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, 32), cdiv(Dp, 32), (unsigned)(a.B * a.Hv)),
                        dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
