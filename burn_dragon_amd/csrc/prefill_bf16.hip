@@ -333,11 +333,16 @@ struct TableKey {
            pos0 == o.pos0 && fixed == o.fixed;
   }
 };
+// A graph captured with the table build in it rewrites the buffer on every
+// replay, unseen by the host: once a capture has happened on a device, its
+// table is rebuilt on every call.
 std::mutex g_table_mu;
 std::map<int, TableKey> g_table;
+std::map<int, bool> g_table_off;
 
 bool table_built(int dev, const TableKey& k) {
   std::lock_guard<std::mutex> lock(g_table_mu);
+  if (g_table_off[dev]) return false;
   auto it = g_table.find(dev);
   return it != g_table.end() && it->second == k;
 }
@@ -345,6 +350,11 @@ bool table_built(int dev, const TableKey& k) {
 void table_record(int dev, const TableKey& k) {
   std::lock_guard<std::mutex> lock(g_table_mu);
   g_table[dev] = k;
+}
+
+void table_reuse_off(int dev) {
+  std::lock_guard<std::mutex> lock(g_table_mu);
+  g_table_off[dev] = true;
 }
 
 }  // namespace
@@ -458,8 +468,12 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   uint64_t n_launch = 1;
   int dev = 0;
   BDH_HIP_TRY(hipGetDevice(&dev));
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  BDH_HIP_TRY(hipStreamIsCapturing(st, &cap));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  if (capturing && rope) table_reuse_off(dev);
   const TableKey tkey{cs, scratch_epoch(SLOT_ROPE_TABLE), a.freqs, a.T, half, a.pos0, a.fixed};
-  if (rope && !table_built(dev, tkey)) {
+  if (rope && (capturing || !table_built(dev, tkey))) {
     const int64_t ntr = (Tp / 32) * (Dp / 32) * a.B * a.Hv;
     hipLaunchKernelGGL(prep_bf16_kernel, dim3((unsigned)ntr + cdiv(a.T * half, 256)), dim3(256), 0, st,
                        a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp, a.B * a.Hv, a.freqs, (uint32_t*)cs, half,
