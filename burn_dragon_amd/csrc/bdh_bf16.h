@@ -152,6 +152,13 @@ struct PrefillArgs {
   int64_t rd_t0, rd_Lc;
   int rd_kr;            // N splits (N/32 a multiple of 2 rd_kr)
   int rd_units;         // prefill_readout_units(S, rd_Lc, D, rd_kr), or 0
+  // add units: ctx[s, add_t0 + t, :] += sum of the previous interval's rd_kr
+  // readout partials (add_src, same layout as rd_part), run in this launch's
+  // tail
+  const float* add_src;
+  float* add_ctx;       // [S, T, D]
+  int64_t add_t0, add_Lc;
+  int add_units;
 };
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
 // Workgroup ids a gram launch needs for `groups` groups of nb-block

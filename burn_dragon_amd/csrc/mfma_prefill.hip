@@ -322,6 +322,46 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
 }
 
 // ---------------------------------------------------------------------------
+// add unit aid: a contiguous share of the previous interval's (s, t, float4)
+// context elements; the partials are summed in split order onto ctx (the
+// order of readout_add_kernel).
+__device__ __forceinline__ void add_unit(const PrefillArgs& a, int aid) {
+  const int64_t d4n = a.D / 4, total = a.S * a.add_Lc * d4n;
+  const int64_t per = (total + a.add_units - 1) / a.add_units;
+  const int64_t b = (int64_t)aid * per, e = b + per < total ? b + per : total;
+  for (int64_t i = b + threadIdx.x; i < e; i += NT) {
+    const int64_t s = i / (a.add_Lc * d4n);
+    const int64_t rem = i - s * a.add_Lc * d4n;
+    const int64_t t = rem / d4n, d = (rem - t * d4n) * 4;
+    float* dst = a.add_ctx + (s * a.T + a.add_t0 + t) * a.D + d;
+    float4 v = *reinterpret_cast<const float4*>(dst);
+    const float* src = a.add_src + (s * a.Lp + t) * a.D + d;
+    const int64_t stride = a.S * a.Lp * a.D;
+    int kp = 0;
+    for (; kp + 4 <= a.rd_kr; kp += 4) {  // four partials' loads in flight
+      float4 r[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const float4*>(src + (kp + j) * stride);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v.x += r[j].x;
+        v.y += r[j].y;
+        v.z += r[j].z;
+        v.w += r[j].w;
+      }
+    }
+    for (; kp < a.rd_kr; ++kp) {
+      const float4 r = *reinterpret_cast<const float4*>(src + kp * stride);
+      v.x += r.x;
+      v.y += r.y;
+      v.z += r.z;
+      v.w += r.w;
+    }
+    *reinterpret_cast<float4*>(dst) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Gram units of one interval.  Units u < nb^2 are the tiles of 256-row block
 // rbk (of nb) x 128-column block cbk for cbk <= 2 rbk, row block by row
 // block.  The block's last column tile (cbk = 2 rbk + 1) has work only in its
@@ -389,7 +429,10 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
     else readout_unit<ROPE, DECAY, false>(a, lds, s, kp, r0, d0);
   } else {
     const int sid = id - a.gram_ids - a.rd_units;
-    if (sid >= a.state_units) return;
+    if (sid >= a.state_units) {
+      if (sid - a.state_units < a.add_units) add_unit(a, sid - a.state_units);
+      return;
+    }
     const int nt = (int)(a.N / (T256 / 2));
     const int dt = (int)((a.D + T256 - 1) / T256);
     const int64_t s = sid / (nt * dt);
@@ -418,7 +461,7 @@ int prefill_readout_units(int64_t S, int64_t Lc, int64_t D, int kr) {
 }
 
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st) {
-  const unsigned grid = (unsigned)(a.gram_ids + a.rd_units + a.state_units);
+  const unsigned grid = (unsigned)(a.gram_ids + a.rd_units + a.state_units + a.add_units);
   if (grid == 0) return hipSuccess;
   const bool decay = a.decay != nullptr;
   if (rope) {

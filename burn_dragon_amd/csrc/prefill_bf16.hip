@@ -452,7 +452,9 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     if (stt != BDH_OK) return stt;
   }
   if (carried) {
-    stt = scratch(SLOT_READOUT, (size_t)(rd_kr * S * Lp * a.D) * sizeof(float), &rdp);
+    // Two buffers: interval iv's partials go to buffer iv % 2, and their add
+    // runs in the next launch, beside that launch's own readout units.
+    stt = scratch(SLOT_READOUT, (size_t)(2 * rd_kr * S * Lp * a.D) * sizeof(float), &rdp);
     if (stt != BDH_OK) return stt;
   }
   if (a.state && n_iv > 1) {
@@ -511,13 +513,32 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   p.Tp = Tp; p.Dp = Dp;
   p.rd_part = (float*)rdp;
   p.rd_kr = rd_kr;
+  p.add_units = 0;
 
   // rho_iv for iv = 0 .. n_iv: rho_in, then the scratch buffers A, B, A, ...,
   // and rho_out for the last.  The readout and state units of interval iv
   // both read rho_iv; the state units write rho_{iv+1}, a different buffer
   // except for a single in-place interval, where they run after the readout.
+  // The readout add of interval iv runs as add units in the tail of launch
+  // iv + 1 (slots freed by its finished units); the last interval's add is
+  // a kernel of its own.
+  const int64_t rd_buf = rd_kr * S * Lp * a.D;
+  int64_t pend_t0 = -1, pend_Lc = 0;
+  int pend_buf = 0;
+  p.add_ctx = a.ctx;
   const float* cur = a.rho_in;
   for (int64_t iv = 0; iv < n_iv; ++iv) {
+    const int buf = (int)(iv & 1);
+    p.rd_part = (float*)rdp + buf * rd_buf;
+    p.add_units = 0;
+    if (pend_t0 >= 0) {
+      p.add_src = (const float*)rdp + pend_buf * rd_buf;
+      p.add_t0 = pend_t0;
+      p.add_Lc = pend_Lc;
+      const int64_t f4 = S * pend_Lc * (a.D / 4);
+      p.add_units = (int)cdiv(f4, 256);  // one float4 of context per thread
+      pend_t0 = -1;
+    }
     const int64_t t0 = iv * L;
     const int64_t Lc = (a.T - t0 < L) ? a.T - t0 : L;
     float* next = iv == n_iv - 1 ? a.rho_out : (float*)(iv % 2 == 0 ? rho_a : rho_b);
@@ -541,6 +562,7 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
       PrefillArgs q = p;
       q.gram_ids = 0;
       q.rd_units = 0;
+      q.add_units = 0;
       q.state_units = state_units;
       kt = ktime_begin(BDH_KERNEL_PREFILL, st);
       BDH_HIP_TRY(launch_prefill_mfma(q, rope, st));
@@ -556,10 +578,16 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
       ++n_launch;
     }
     if (cur) {
-      hipLaunchKernelGGL(readout_add_kernel, dim3(cdiv(S * Lc * (a.D / 4), 256)), dim3(256), 0, st,
-                         (const float*)rdp, a.ctx, S, a.T, a.D, t0, Lc, Lp, rd_kr);
-      BDH_HIP_TRY(hipGetLastError());
-      ++n_launch;
+      if (a.state && iv + 1 < n_iv) {
+        pend_t0 = t0;
+        pend_Lc = Lc;
+        pend_buf = buf;
+      } else {
+        hipLaunchKernelGGL(readout_add_kernel, dim3(cdiv(S * Lc * (a.D / 4), 256)), dim3(256), 0, st,
+                           (const float*)p.rd_part, a.ctx, S, a.T, a.D, t0, Lc, Lp, rd_kr);
+        BDH_HIP_TRY(hipGetLastError());
+        ++n_launch;
+      }
     }
     if (!a.state) break;  // dense mode: one interval, no state
     cur = next;
