@@ -213,18 +213,25 @@ constexpr int SK_CHUNK = 8;  // 32-deep steps loaded at once per wave
 
 template <int KIND, int MB>  // MB = 16-row blocks: 1, 2 or 4
 __global__ __launch_bounds__(256) void skinny_gemm_kernel(LayerGemmArgs g) {
-  __shared__ floatx4 red[4][MB][64];
+  // X, Y (K = D, H N columns): each wave owns a 16-column block and all of
+  // K.  Z (K = H N) and the logits (few columns): the workgroup owns one
+  // column block and a K range, which its 4 waves split and sum through LDS
+  // in wave order.  (X, Y: 13 and 15 -> 11 us at C5 decode.)
+  constexpr bool WAVECOL = KIND == G_X || KIND == G_Y;
+  __shared__ floatx4 red[WAVECOL ? 1 : 4][MB][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t ncols = KIND == G_Z ? g.D : KIND == G_L ? g.V : g.H * g.N;
   const int64_t K = KIND == G_Z ? g.H * g.N : g.D;
   const int ncb = (int)((ncols + 15) / 16);
-  const int cblk = (int)(blockIdx.x % ncb), kp = (int)(blockIdx.x / ncb);
+  const int cblk = WAVECOL ? (int)blockIdx.x * 4 + w : (int)(blockIdx.x % ncb);
+  const int kp = WAVECOL ? 0 : (int)(blockIdx.x / ncb);
+  if (WAVECOL && cblk >= ncb) return;  // no barriers in this mode
   const int64_t c0 = (int64_t)cblk * 16;
   const int64_t h = (KIND == G_X || KIND == G_Y) ? c0 / g.N : 0;
-  // Steps of this wave: part p of 4 * ks equal parts of the K/32 steps.
+  // Steps of this wave: all K/32 (WAVECOL), or part p of 4 * ks equal parts.
   const int64_t nk = K / 32, parts = 4 * (int64_t)g.ks, p = (int64_t)kp * 4 + w;
-  const int kb = (int)(nk * p / parts), ke = (int)(nk * (p + 1) / parts);
-
+  const int kb = WAVECOL ? 0 : (int)(nk * p / parts);
+  const int ke = WAVECOL ? (int)nk : (int)(nk * (p + 1) / parts);
   const int kl = 8 * (lane >> 4);  // this lane's 8 k values within a step
   int64_t cb = c0 + (lane & 15);
   cb = cb < ncols ? cb : ncols - 1;
@@ -262,54 +269,61 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(LayerGemmArgs g) {
       for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16(aq[s][mb], bq[s], acc[mb]);
     }
   }
+  const int64_t c = c0 + (lane & 15);
+  const int64_t n = c - h * g.N;
+  // Epilogue of the 16 x 16 block of row block mb (lane: rows
+  // 4 (lane >> 4) + r, column lane & 15).
+  auto emit = [&](int mb, const floatx4& v) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t m = 16 * mb + acc16_row(lane, r);
+      float val = v[r];
+      if (KIND == G_X) {
+        // Every lane joins the partner exchange before any row test.
+        const float x = fmaxf(val, 0.0f);
+        const float xp = __shfl_xor(x, 1, 64);  // column c ^ 1 of the same row
+        if (m >= g.M) continue;
+        const int64_t bb = m / g.T, t = m - bb * g.T;
+        const int64_t o = ((bb * g.H + h) * g.T + t) * g.N + n;
+        g.xy[o] = (bf16_t)x;
+        if (g.xf) g.xf[o] = x;
+        if (g.q) {
+          const float p = (float)(g.fixed ? g.pos0 : g.pos0 + t);
+          const int64_t ne = n & ~(int64_t)1;
+          const float fr = rope_frac(p, g.freqs[ne]);
+          const float e = (n & 1) ? xp : x, od = (n & 1) ? x : xp;
+          float qe, qo;
+          rope_pair_exact(e, od, __builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr), qe, qo);
+          g.q[o] = (bf16_t)((n & 1) ? qo : qe);
+        }
+      } else {
+        if (m >= g.M) continue;
+        if (KIND == G_Y) {
+          const int64_t bb = m / g.T, t = m - bb * g.T;
+          bf16_t* dst = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
+          *dst = (bf16_t)(fmaxf(val, 0.0f) * (float)*dst);
+        } else if (KIND == G_Z) {
+          g.zpart[((int64_t)kp * g.M + m) * g.D + c] = val;
+        } else if (c < g.V) {
+          g.zpart[m * g.V + c] = val;
+        }
+      }
+    }
+  };
+  if (WAVECOL) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) emit(mb, acc[mb]);
+    return;
+  }
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) red[w][mb][lane] = acc[mb];
   __syncthreads();
-  // Wave mb finishes row block mb: the 4 wave partials in order, then the
-  // epilogue of the 16 x 16 block (lane: rows 4 (lane >> 4) + r, column
-  // lane & 15).
-  const int mb = w;
-  if (mb >= MB) return;
-  floatx4 v = red[0][mb][lane];
+  // Wave mb finishes row block mb: the 4 wave partials in order.
+  if (w >= MB) return;
+  floatx4 v = red[0][w][lane];
 #pragma unroll
-  for (int ww = 1; ww < 4; ++ww) v = v + red[ww][mb][lane];
-  const int64_t c = c0 + (lane & 15);
-  const int64_t n = c - h * g.N;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t m = 16 * mb + acc16_row(lane, r);
-    float val = v[r];
-    if (KIND == G_X) {
-      // Every lane joins the partner exchange before any row test.
-      const float x = fmaxf(val, 0.0f);
-      const float xp = __shfl_xor(x, 1, 64);  // column c ^ 1 of the same row
-      if (m >= g.M) continue;
-      const int64_t bb = m / g.T, t = m - bb * g.T;
-      const int64_t o = ((bb * g.H + h) * g.T + t) * g.N + n;
-      g.xy[o] = (bf16_t)x;
-      if (g.xf) g.xf[o] = x;
-      if (g.q) {
-        const float p = (float)(g.fixed ? g.pos0 : g.pos0 + t);
-        const int64_t ne = n & ~(int64_t)1;
-        const float fr = rope_frac(p, g.freqs[ne]);
-        const float e = (n & 1) ? xp : x, od = (n & 1) ? x : xp;
-        float qe, qo;
-        rope_pair_exact(e, od, __builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr), qe, qo);
-        g.q[o] = (bf16_t)((n & 1) ? qo : qe);
-      }
-    } else {
-      if (m >= g.M) continue;
-      if (KIND == G_Y) {
-        const int64_t bb = m / g.T, t = m - bb * g.T;
-        bf16_t* dst = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
-        *dst = (bf16_t)(fmaxf(val, 0.0f) * (float)*dst);
-      } else if (KIND == G_Z) {
-        g.zpart[((int64_t)kp * g.M + m) * g.D + c] = val;
-      } else if (c < g.V) {
-        g.zpart[m * g.V + c] = val;
-      }
-    }
-  }
+  for (int ww = 1; ww < 4; ++ww) v = v + red[ww][w][lane];
+  emit(w, v);
 }
 
 // Wave-wide sum (fixed butterfly order: the same result in every lane).
@@ -454,7 +468,8 @@ inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b);
 template <int KIND>
 hipError_t launch_skinny(const LayerGemmArgs& g, hipStream_t st) {
   const int64_t ncols = KIND == G_Z ? g.D : KIND == G_L ? g.V : g.H * g.N;
-  const int64_t blocks = cdiv(ncols, 16) * (int64_t)(KIND == G_Z ? g.ks : 1);
+  const int64_t blocks = (KIND == G_X || KIND == G_Y) ? cdiv(cdiv(ncols, 16), 4)
+                                                      : cdiv(ncols, 16) * (int64_t)(KIND == G_Z ? g.ks : 1);
   const dim3 grid((unsigned)blocks);
   if (g.M <= 16) hipLaunchKernelGGL((skinny_gemm_kernel<KIND, 1>), grid, dim3(256), 0, st, g);
   else if (g.M <= 32) hipLaunchKernelGGL((skinny_gemm_kernel<KIND, 2>), grid, dim3(256), 0, st, g);
