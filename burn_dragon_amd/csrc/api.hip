@@ -33,7 +33,6 @@ namespace {
 struct DeviceScratch {
   void* ptr[SLOT_COUNT] = {};
   size_t bytes[SLOT_COUNT] = {};
-  uint64_t epoch[SLOT_COUNT] = {};  // (re)allocations of the slot
   std::map<std::pair<int64_t, uint32_t>, float*> freqs;
 };
 std::mutex g_scratch_mu;
@@ -62,18 +61,11 @@ bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc) {
     if (zero_on_alloc) BDH_HIP_TRY(hipMemset(p, 0, grow));
     ds.ptr[slot] = p;
     ds.bytes[slot] = grow;
-    ++ds.epoch[slot];
   }
   *out = ds.ptr[slot];
   return BDH_OK;
 }
 
-uint64_t scratch_epoch(int slot) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return ~0ull;
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  return device_scratch(dev).epoch[slot];
-}
 
 // ------------------------------------------------------------------ RoPE ----
 // Attention::build_freqs, Rope arm (attention.rs:559-563), in f32:

@@ -159,6 +159,10 @@ struct PrefillArgs {
   float* add_ctx;       // [S, T, D]
   int64_t add_t0, add_Lc;
   int add_units;
+  // table_key, if set: workgroup 0 writes table_key_val there (the key of
+  // the (cos, sin) table this launch reads)
+  int64_t* table_key;
+  int64_t table_key_val[6];
 };
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
 // Workgroup ids a gram launch needs for `groups` groups of nb-block

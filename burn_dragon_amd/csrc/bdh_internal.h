@@ -26,7 +26,7 @@ bdh_status hip_fail(hipError_t e, const char* what);
 enum ScratchSlot {
   SLOT_SCORES = 0,   // causal score partials    [KS, S, n_iv, Lp, Lp] f32
   SLOT_VT,           // transposed values        [B*Hv, Dp, Tp] bf16
-  SLOT_ROPE_TABLE,   // packed bf16 cos/sin per (token, pair) [T, N/2]
+  SLOT_ROPE_TABLE,   // table key (8 int64), then packed bf16 cos/sin per (token, pair) [T, N/2]
   SLOT_ROTATED,      // rotated queries [S, T, N]: f32 (fp32 path) or bf16 (bf16 path)
   SLOT_READOUT,      // readout partials (bf16 path) [rd_kr, S, Lp, D] f32
   SLOT_RHO_A,        // states between intervals (bf16 path) [S, N, D] f32
@@ -44,9 +44,6 @@ enum ScratchSlot {
   SLOT_COUNT
 };
 bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);
-// Number of (re)allocations of a slot on the current device: contents kept
-// across calls are valid only while it is unchanged.
-uint64_t scratch_epoch(int slot);
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus();

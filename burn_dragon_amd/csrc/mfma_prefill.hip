@@ -383,6 +383,14 @@ template <bool ROPE, bool DECAY>
 __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[2 * BUF];
   const int id = blockIdx.x;
+  // The table was complete before this launch began; name it for the next
+  // call's prep kernel.
+  // (Static indices: indexing the kernel argument by thread would copy it to
+  // private memory.)
+  if (a.table_key && id == 0 && threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i) a.table_key[i] = a.table_key_val[i];
+  }
   if (id < a.gram_ids) {
     const int tpg = units_per_group(a.nb);
     const int blk = id / (8 * tpg), rem = id - blk * 8 * tpg;

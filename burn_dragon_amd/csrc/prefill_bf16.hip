@@ -18,9 +18,6 @@
 // RoPE is applied to Q tiles between HBM and LDS from a packed bf16
 // (cos, sin) table of the call's (token, pair) phases; rotated queries are
 // never written to memory.
-#include <map>
-#include <mutex>
-
 #include "bdh_bf16.h"
 
 namespace bdh {
@@ -264,6 +261,12 @@ __device__ __forceinline__ void rope_table_entry(const float* __restrict__ freqs
   cs[i] = pack_bf16x2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
 }
 
+// The table buffer starts with TABLE_KEY_WORDS int64 words naming the table
+// it holds: magic, T, N/2, first position, fixed flag, frequency pointer
+// (zero on allocation, so a new buffer matches nothing).
+constexpr int TABLE_KEY_WORDS = 8;
+constexpr int64_t TABLE_KEY_MAGIC = 0x62646874626c0001LL;
+
 // V^T and the RoPE table in one launch (both are short and independent):
 // workgroups [0, ntr) are transpose tiles (t fastest, then d, then slab), the
 // rest 256 table entries each.
@@ -280,6 +283,13 @@ __global__ __launch_bounds__(256) void prep_bf16_kernel(const bf16_t* __restrict
     transpose_v_tile(v, vt, T, D, Tp, Dp, id / (gt * gd), (tile % gt) * 32, (tile / gt) * 32);
     return;
   }
+  // The table depends only on (positions, frequencies): when the key kept in
+  // front of it (written by the previous prefill launch that used it) is
+  // this call's, the entries are already there.
+  const int64_t* key = reinterpret_cast<const int64_t*>(cs) - TABLE_KEY_WORDS;
+  if (key[0] == TABLE_KEY_MAGIC && key[1] == T && key[2] == half && key[3] == pos_first &&
+      key[4] == fixed && key[5] == reinterpret_cast<int64_t>(freqs))
+    return;
   const int64_t i = (id - ntr) * 256 + threadIdx.x;
   if (i < T * half) rope_table_entry(freqs, cs, i, half, pos_first, fixed);
 }
@@ -318,44 +328,6 @@ __global__ __launch_bounds__(256) void rope_rotate_bf16_kernel(const bf16_t* __r
 }
 
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
-
-// The RoPE table depends only on the positions and the frequencies: a call
-// whose key matches the table last built in the device's table buffer reuses
-// it (prefills of new sequences all start at position 0).
-struct TableKey {
-  const void* buf;
-  uint64_t epoch;  // of the table's scratch slot: a reallocation invalidates
-  const float* freqs;
-  int64_t T, half, pos0;
-  int fixed;
-  bool operator==(const TableKey& o) const {
-    return buf == o.buf && epoch == o.epoch && freqs == o.freqs && T == o.T && half == o.half &&
-           pos0 == o.pos0 && fixed == o.fixed;
-  }
-};
-// A graph captured with the table build in it rewrites the buffer on every
-// replay, unseen by the host: once a capture has happened on a device, its
-// table is rebuilt on every call.
-std::mutex g_table_mu;
-std::map<int, TableKey> g_table;
-std::map<int, bool> g_table_off;
-
-bool table_built(int dev, const TableKey& k) {
-  std::lock_guard<std::mutex> lock(g_table_mu);
-  if (g_table_off[dev]) return false;
-  auto it = g_table.find(dev);
-  return it != g_table.end() && it->second == k;
-}
-
-void table_record(int dev, const TableKey& k) {
-  std::lock_guard<std::mutex> lock(g_table_mu);
-  g_table[dev] = k;
-}
-
-void table_reuse_off(int dev) {
-  std::lock_guard<std::mutex> lock(g_table_mu);
-  g_table_off[dev] = true;
-}
 
 }  // namespace
 
@@ -448,8 +420,11 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     stt = scratch(SLOT_ROTATED, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xr);
     if (stt != BDH_OK) return stt;
   } else if (a.freqs) {
-    stt = scratch(SLOT_ROPE_TABLE, (size_t)(a.T * half) * sizeof(uint32_t), &cs);
+    void* tb = nullptr;
+    stt = scratch(SLOT_ROPE_TABLE, TABLE_KEY_WORDS * sizeof(int64_t) + (size_t)(a.T * half) * sizeof(uint32_t),
+                  &tb, true);
     if (stt != BDH_OK) return stt;
+    cs = (char*)tb + TABLE_KEY_WORDS * sizeof(int64_t);
   }
   if (carried) {
     // Two buffers: interval iv's partials go to buffer iv % 2, and their add
@@ -468,20 +443,11 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   const bool rope = a.freqs != nullptr && !prerot;
 
   uint64_t n_launch = 1;
-  int dev = 0;
-  BDH_HIP_TRY(hipGetDevice(&dev));
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  BDH_HIP_TRY(hipStreamIsCapturing(st, &cap));
-  const bool capturing = cap != hipStreamCaptureStatusNone;
-  if (capturing && rope) table_reuse_off(dev);
-  const TableKey tkey{cs, scratch_epoch(SLOT_ROPE_TABLE), a.freqs, a.T, half, a.pos0, a.fixed};
-  if (rope && (capturing || !table_built(dev, tkey))) {
+  if (rope) {
     const int64_t ntr = (Tp / 32) * (Dp / 32) * a.B * a.Hv;
     hipLaunchKernelGGL(prep_bf16_kernel, dim3((unsigned)ntr + cdiv(a.T * half, 256)), dim3(256), 0, st,
                        a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp, a.B * a.Hv, a.freqs, (uint32_t*)cs, half,
                        a.pos0, a.fixed);
-    BDH_HIP_TRY(hipGetLastError());
-    table_record(dev, tkey);
   } else {
     hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, 32), cdiv(Dp, 32), (unsigned)(a.B * a.Hv)),
                        dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
@@ -503,6 +469,13 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   PrefillArgs p{};
   p.x = prerot ? (const bf16_t*)xr : a.x;
   p.cs = (const uint32_t*)cs;
+  if (rope) {
+    // The first prefill launch records which table the buffer now holds.
+    p.table_key = reinterpret_cast<int64_t*>((char*)cs - TABLE_KEY_WORDS * sizeof(int64_t));
+    const int64_t k[6] = {TABLE_KEY_MAGIC, a.T, half, a.pos0, a.fixed,
+                          reinterpret_cast<int64_t>(a.freqs)};
+    for (int i = 0; i < 6; ++i) p.table_key_val[i] = k[i];
+  }
   p.decay = a.decay;
   p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;
   p.part = (float*)part;
@@ -557,6 +530,7 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     int kt = ktime_begin(BDH_KERNEL_PREFILL, st);
     BDH_HIP_TRY(launch_prefill_mfma(p, rope, st));
     ktime_end(kt, st);
+    p.table_key = nullptr;
     ++n_launch;
     if (a.state && in_place) {
       PrefillArgs q = p;

@@ -1,7 +1,6 @@
-"""HIP graph capture of the bf16 prefill.  Kept in a file that sorts after
-the other GPU tests: a capture turns off the reuse of the RoPE table for the
-rest of the process (replays rewrite it unseen), and the table-reuse test in
-test_gpu_prefill.py should run with reuse on."""
+"""HIP graph capture of the bf16 prefill: replays interleaved with eager
+calls at other positions, so the RoPE table (kept across calls and named by
+a key in device memory) is rebuilt and reused in both directions."""
 import pytest
 
 from tests.gpu_util import announce, need_gpu
