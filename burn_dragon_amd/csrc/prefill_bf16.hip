@@ -297,34 +297,47 @@ __global__ __launch_bounds__(256) void prep_bf16_kernel(const bf16_t* __restrict
 // q[s, t, :] = rope(x[s, t, :]) in bf16: phase frac(p f) in the reference's
 // f32 op order, cos / sin by v_cos_f32 / v_sin_f32 of it, the rotation in f32
 // in the op order of attention.rs:488-501, then rounded to bf16.  Workgroup b
-// covers 2048 elements (8 a lane) of row row0 + b / segs, so the row and its
-// position are workgroup-uniform (scalar arithmetic).
+// covers 2048 elements (8 a lane) of the ROT_ROWS rows row0 + ROT_ROWS (b /
+// segs) + r (r < ROT_ROWS, rows < row_end): one frequency load and ROT_ROWS
+// x loads in flight per lane, rows and positions workgroup-uniform (scalar
+// arithmetic).  q is written with streaming stores: it is read by later
+// launches, after far more than the caches hold has passed through them.
 constexpr int ROT_SEG = 2048;
+constexpr int ROT_ROWS = 4;
 __global__ __launch_bounds__(256) void rope_rotate_bf16_kernel(const bf16_t* __restrict__ x,
                                                                const float* __restrict__ freqs,
                                                                bf16_t* __restrict__ q, int64_t row0,
-                                                               int64_t segs, int64_t T, int64_t N,
-                                                               int64_t pos_first, int fixed) {
+                                                               int64_t row_end, int64_t segs, int64_t T,
+                                                               int64_t N, int64_t pos_first, int fixed) {
   const int64_t b = blockIdx.x / segs;
   const int64_t n = (blockIdx.x - b * segs) * ROT_SEG + threadIdx.x * 8;
-  const int64_t row = row0 + b;
+  const int64_t rb = row0 + b * ROT_ROWS;
   if (n >= N) return;  // N % 8 == 0: a lane's 8 elements are all in the row or all past it
-  const float p = (float)(fixed ? pos_first : pos_first + row % T);
-  const uint4 raw = *reinterpret_cast<const uint4*>(x + row * N + n);
   const float4 f0 = *reinterpret_cast<const float4*>(freqs + n);
   const float4 f1 = *reinterpret_cast<const float4*>(freqs + n + 4);
-  const uint32_t in[4] = {raw.x, raw.y, raw.z, raw.w};
   const float f[4] = {f0.x, f0.z, f1.x, f1.z};  // one frequency per pair
-  uint32_t out[4];
+  uint4 raw[ROT_ROWS];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float fr = rope_frac(p, f[k]);
-    float e, o;
-    rope_pair_exact(bf16_lo(in[k]), bf16_hi(in[k]), __builtin_amdgcn_cosf(fr),
-                    __builtin_amdgcn_sinf(fr), e, o);
-    out[k] = pack_bf16x2(e, o);
+  for (int r = 0; r < ROT_ROWS; ++r)
+    if (rb + r < row_end) raw[r] = *reinterpret_cast<const uint4*>(x + (rb + r) * N + n);
+#pragma unroll
+  for (int r = 0; r < ROT_ROWS; ++r) {
+    const int64_t row = rb + r;
+    if (row >= row_end) break;
+    const float p = (float)(fixed ? pos_first : pos_first + row % T);
+    const uint32_t in[4] = {raw[r].x, raw[r].y, raw[r].z, raw[r].w};
+    uint32_t out[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float fr = rope_frac(p, f[k]);
+      float e, o;
+      rope_pair_exact(bf16_lo(in[k]), bf16_hi(in[k]), __builtin_amdgcn_cosf(fr),
+                      __builtin_amdgcn_sinf(fr), e, o);
+      out[k] = pack_bf16x2(e, o);
+    }
+    __builtin_nontemporal_store(u32x4{out[0], out[1], out[2], out[3]},
+                                reinterpret_cast<u32x4*>(q + row * N + n));
   }
-  *reinterpret_cast<uint4*>(q + row * N + n) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
@@ -456,11 +469,11 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   if (prerot) {
     // Launches of at most 2^22 workgroups (2^30 work-items) each.
     const int64_t segs = cdiv(a.N, ROT_SEG);
-    const int64_t rows_per = ((int64_t)1 << 22) / segs;
+    const int64_t rows_per = (((int64_t)1 << 22) / segs) * ROT_ROWS;
     for (int64_t r0 = 0; r0 < S * a.T; r0 += rows_per) {
       const int64_t rows = S * a.T - r0 < rows_per ? S * a.T - r0 : rows_per;
-      hipLaunchKernelGGL(rope_rotate_bf16_kernel, dim3((unsigned)(rows * segs)), dim3(256), 0, st,
-                         a.x, a.freqs, (bf16_t*)xr, r0, segs, a.T, a.N, a.pos0, a.fixed);
+      hipLaunchKernelGGL(rope_rotate_bf16_kernel, dim3((unsigned)(cdiv(rows, ROT_ROWS) * segs)), dim3(256),
+                         0, st, a.x, a.freqs, (bf16_t*)xr, r0, r0 + rows, segs, a.T, a.N, a.pos0, a.fixed);
       BDH_HIP_TRY(hipGetLastError());
       ++n_launch;
     }

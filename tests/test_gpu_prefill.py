@@ -116,6 +116,7 @@ def _bf16_case(rng, B, H, Hv, T, N, D, with_rho):
     (1, 4, 1, 256, 256, 64, True, [0.99, 0.98, 0.97, 0.96], 0),  # ALiBi-style decay
     (1, 2, 1, 700, 512, 320, True, [0.995, 0.99], 9),  # D > 256, not a multiple of 256; 2 intervals
     (2, 2, 1, 600, 2304, 64, False, None, 5),          # x rotated once: rows of 4 streams, N % 2048 != 0
+    (1, 1, 1, 1027, 256, 64, True, None, 2),           # x rotated once: B H T not a multiple of 4 rows
 ])
 def test_bf16_rope_prefill_matches_oracle(oracle, B, H, Hv, T, N, D, with_rho, decay, pos):
     torch = need_gpu()
