@@ -225,26 +225,47 @@ __global__ __launch_bounds__(256) void readout_add_kernel(const float* __restric
 
 // vt[bv, d, t] = v[bv, t, d] for t < T, d < D; 0 for T <= t < Tp or D <= d < Dp:
 // the 32 x 32 tile (t0, d0) of slab bv.
+// One 64 x 64 tile of v^T (tokens t0 .., columns d0 ..): 16-byte loads of v
+// rows (8 columns; D is a multiple of 32, so 8 columns are all inside D or
+// all past it) into LDS, 16-byte stores of v^T rows (8 tokens; Tp is a
+// multiple of 128).  Zeros past T and D.
+constexpr int VT_TILE = 64;
 __device__ __forceinline__ void transpose_v_tile(const bf16_t* __restrict__ v, bf16_t* __restrict__ vt,
                                                  int64_t T, int64_t D, int64_t Tp, int64_t Dp,
                                                  int64_t bv, int64_t t0, int64_t d0) {
-  __shared__ bf16_t tile[32][33];
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
-  for (int r = ty; r < 32; r += 8) {
-    const int64_t t = t0 + r, d = d0 + tx;
-    tile[r][tx] = (t < T && d < D) ? v[(bv * T + t) * D + d] : (bf16_t)0.0f;
+  __shared__ __attribute__((aligned(16))) uint32_t tile[VT_TILE][VT_TILE / 2 + 1];  // [t][d pair]
+  const int tid = threadIdx.x;
+  for (int i = tid; i < VT_TILE * 8; i += 256) {
+    const int r = i >> 3, c = (i & 7) * 8;
+    const int64_t t = t0 + r, d = d0 + c;
+    uint4 e = make_uint4(0, 0, 0, 0);
+    if (t < T && d < D) e = *reinterpret_cast<const uint4*>(v + (bv * T + t) * D + d);
+    tile[r][c / 2] = e.x;
+    tile[r][c / 2 + 1] = e.y;
+    tile[r][c / 2 + 2] = e.z;
+    tile[r][c / 2 + 3] = e.w;
   }
   __syncthreads();
-  for (int r = ty; r < 32; r += 8) {
-    const int64_t d = d0 + r, t = t0 + tx;
-    if (d < Dp && t < Tp) vt[(bv * Dp + d) * Tp + t] = tile[tx][r];
+  for (int i = tid; i < VT_TILE * 8; i += 256) {
+    const int r = i >> 3, c = (i & 7) * 8;  // v^T row d0 + r, tokens t0 + c ..
+    const int64_t d = d0 + r, t = t0 + c;
+    if (d >= Dp || t >= Tp) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = tile[c + 2 * j][r >> 1], b = tile[c + 2 * j + 1][r >> 1];
+      // element r of tokens c + 2j and c + 2j + 1: the low or high half of their words
+      w[j] = (r & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+    }
+    *reinterpret_cast<uint4*>(vt + (bv * Dp + d) * Tp + t) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
 __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restrict__ v,
                                                           bf16_t* __restrict__ vt, int64_t T,
                                                           int64_t D, int64_t Tp, int64_t Dp) {
-  transpose_v_tile(v, vt, T, D, Tp, Dp, blockIdx.z, (int64_t)blockIdx.x * 32, (int64_t)blockIdx.y * 32);
+  transpose_v_tile(v, vt, T, D, Tp, Dp, blockIdx.z, (int64_t)blockIdx.x * VT_TILE,
+                   (int64_t)blockIdx.y * VT_TILE);
 }
 
 // Packed bf16 (cos, sin) of the RoPE phase of (token, pair) i: low half cos.
@@ -269,18 +290,20 @@ constexpr int64_t TABLE_KEY_MAGIC = 0x62646874626c0001LL;
 
 // V^T and the RoPE table in one launch (both are short and independent):
 // workgroups [0, ntr) are transpose tiles (t fastest, then d, then slab), the
-// rest 256 table entries each.
+// rest TBL_PER_WG table entries each (TBL_PER_WG / 256 a thread, so that
+// few workgroups are launched just to find the table already built).
+constexpr int TBL_PER_WG = 4096;
 __global__ __launch_bounds__(256) void prep_bf16_kernel(const bf16_t* __restrict__ v,
                                                         bf16_t* __restrict__ vt, int64_t T,
                                                         int64_t D, int64_t Tp, int64_t Dp,
                                                         int64_t slabs, const float* __restrict__ freqs,
                                                         uint32_t* __restrict__ cs, int64_t half,
                                                         int64_t pos_first, int fixed) {
-  const int64_t gt = Tp / 32, gd = Dp / 32, ntr = gt * gd * slabs;
+  const int64_t gt = Tp / VT_TILE, gd = Dp / VT_TILE, ntr = gt * gd * slabs;
   const int64_t id = blockIdx.x;
   if (id < ntr) {
     const int64_t tile = id % (gt * gd);
-    transpose_v_tile(v, vt, T, D, Tp, Dp, id / (gt * gd), (tile % gt) * 32, (tile / gt) * 32);
+    transpose_v_tile(v, vt, T, D, Tp, Dp, id / (gt * gd), (tile % gt) * VT_TILE, (tile / gt) * VT_TILE);
     return;
   }
   // The table depends only on (positions, frequencies): when the key kept in
@@ -290,8 +313,12 @@ __global__ __launch_bounds__(256) void prep_bf16_kernel(const bf16_t* __restrict
   if (key[0] == TABLE_KEY_MAGIC && key[1] == T && key[2] == half && key[3] == pos_first &&
       key[4] == fixed && key[5] == reinterpret_cast<int64_t>(freqs))
     return;
-  const int64_t i = (id - ntr) * 256 + threadIdx.x;
-  if (i < T * half) rope_table_entry(freqs, cs, i, half, pos_first, fixed);
+  const int64_t i0 = (id - ntr) * TBL_PER_WG + threadIdx.x;
+#pragma unroll 4
+  for (int j = 0; j < TBL_PER_WG / 256; ++j) {
+    const int64_t i = i0 + j * 256;
+    if (i < T * half) rope_table_entry(freqs, cs, i, half, pos_first, fixed);
+  }
 }
 
 // q[s, t, :] = rope(x[s, t, :]) in bf16: phase frac(p f) in the reference's
@@ -457,12 +484,12 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
 
   uint64_t n_launch = 1;
   if (rope) {
-    const int64_t ntr = (Tp / 32) * (Dp / 32) * a.B * a.Hv;
-    hipLaunchKernelGGL(prep_bf16_kernel, dim3((unsigned)ntr + cdiv(a.T * half, 256)), dim3(256), 0, st,
+    const int64_t ntr = (Tp / VT_TILE) * (Dp / VT_TILE) * a.B * a.Hv;
+    hipLaunchKernelGGL(prep_bf16_kernel, dim3((unsigned)ntr + cdiv(a.T * half, TBL_PER_WG)), dim3(256), 0, st,
                        a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp, a.B * a.Hv, a.freqs, (uint32_t*)cs, half,
                        a.pos0, a.fixed);
   } else {
-    hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, 32), cdiv(Dp, 32), (unsigned)(a.B * a.Hv)),
+    hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, VT_TILE), cdiv(Dp, VT_TILE), (unsigned)(a.B * a.Hv)),
                        dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
   }
   BDH_HIP_TRY(hipGetLastError());
