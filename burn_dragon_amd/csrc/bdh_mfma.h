@@ -77,6 +77,7 @@ __device__ __forceinline__ void epilogue_64x128(const floatx4 (&acc)[4][8], bf16
     __syncthreads();
 #pragma unroll
     for (int rr = 0; rr < 16; rr += 2) {
+      // A lane's columns are the same in every call (GEMM X relies on it).
       const int row = rr + (lane >> 5), col = 4 * (lane & 31);
       emit(mi * 16 + row, col, *reinterpret_cast<const float4*>(&E[row * EP + col]));
     }

@@ -145,6 +145,15 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
     return;
   }
 
+  // X with q: a lane's columns are the same in every call of the epilogue
+  // (4 (lane & 31) .. + 3: pairs (n, n+1), (n+2, n+3)), so their two
+  // frequencies are loaded once per tile, not once per call.
+  float fq[2] = {0.0f, 0.0f};
+  if (KIND == G_X && g.q) {
+    const int64_t n0 = c0 + 4 * (lane & 31) - h * g.N;
+    fq[0] = g.freqs[n0];
+    fq[1] = g.freqs[n0 + 2];
+  }
   epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
     const int64_t m = m0 + 64 * w + row, c = c0 + col;
     if (m >= g.M) return;
@@ -181,7 +190,7 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
       float qv[4];
 #pragma unroll
       for (int j = 0; j < 4; j += 2) {
-        const float fr = rope_frac(p, g.freqs[n + j]);
+        const float fr = rope_frac(p, fq[j / 2]);
         rope_pair_exact(r[j], r[j + 1], __builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr),
                         qv[j], qv[j + 1]);
       }
