@@ -85,6 +85,32 @@ __device__ __forceinline__ void epilogue_64x128(const floatx4 (&acc)[4][8], bf16
   }
 }
 
+// As epilogue_64x128 with 8 columns per call: emit(row, col, lo, hi) gets
+// columns col .. col + 3 (lo) and col + 4 .. col + 7 (hi) of one row, with
+// col = 8 (lane & 15) the same in every call and 4 rows per wave call, so a
+// caller writing bf16 issues one 16-byte store per lane and call.
+template <class Emit>
+__device__ __forceinline__ void epilogue8_64x128(const floatx4 (&acc)[4][8], bf16_t* lds, int w,
+                                                 int lane, Emit&& emit) {
+  constexpr int EP = 132;
+  float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) E[acc16_row(lane, r) * EP + ni * 16 + acc16_col(lane)] = acc[mi][ni][r];
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 16; rr += 4) {
+      const int row = rr + (lane >> 4), col = 8 * (lane & 15);
+      emit(mi * 16 + row, col, *reinterpret_cast<const float4*>(&E[row * EP + col]),
+           *reinterpret_cast<const float4*>(&E[row * EP + col + 4]));
+    }
+    __syncthreads();
+  }
+}
+
 // Steps [kb, ke), an even count: LDS buffer (kt - kb) & 1 holds step kt; the
 // loads of step kt+1 are issued before step kt's MFMAs and written to the
 // other buffer after them.

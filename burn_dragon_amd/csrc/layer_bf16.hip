@@ -106,13 +106,14 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
   });
 
   if (KIND == G_Y) {
-    // As epilogue_64x128, with the 8 x reads of a 16-row slice issued
-    // before any y store: y overwrites x in place, so the compiler could not
-    // move one row's load above another row's store, and each read would be
-    // a round trip of its own.
+    // As epilogue8_64x128 (8 columns per lane: 16-byte x reads and y
+    // stores), with the 4 x reads of a 16-row slice issued before any y
+    // store: y overwrites x in place, so the compiler could not move one
+    // row's load above another row's store, and each read would be a round
+    // trip of its own.
     constexpr int EP = 132;
     float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
-    const int col = 4 * (lane & 31);
+    const int col = 8 * (lane & 15);
     const int64_t c = c0 + col, n = c - h * g.N;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
@@ -121,39 +122,80 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
 #pragma unroll
         for (int r = 0; r < 4; ++r) E[acc16_row(lane, r) * EP + ni * 16 + acc16_col(lane)] = acc[mi][ni][r];
       __syncthreads();
-      bf16_t* dst[8];
-      uint2 xv[8];
+      bf16_t* dst[4];
+      uint4 xv[4];
 #pragma unroll
-      for (int rr = 0; rr < 8; ++rr) {
-        int64_t m = m0 + 64 * w + mi * 16 + 2 * rr + (lane >> 5);
+      for (int rr = 0; rr < 4; ++rr) {
+        int64_t m = m0 + 64 * w + mi * 16 + 4 * rr + (lane >> 4);
         m = m < g.M ? m : g.M - 1;  // rows past M re-read the last row, never stored
         const int64_t bb = m / g.T, t = m - bb * g.T;
         dst[rr] = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
-        xv[rr] = *reinterpret_cast<const uint2*>(dst[rr]);
+        xv[rr] = *reinterpret_cast<const uint4*>(dst[rr]);
       }
 #pragma unroll
-      for (int rr = 0; rr < 8; ++rr) {
-        const int row = 2 * rr + (lane >> 5);
-        const float4 v = *reinterpret_cast<const float4*>(&E[row * EP + col]);
-        const float y0 = fmaxf(v.x, 0.0f) * bf16_lo(xv[rr].x), y1 = fmaxf(v.y, 0.0f) * bf16_hi(xv[rr].x);
-        const float y2 = fmaxf(v.z, 0.0f) * bf16_lo(xv[rr].y), y3 = fmaxf(v.w, 0.0f) * bf16_hi(xv[rr].y);
+      for (int rr = 0; rr < 4; ++rr) {
+        const int row = 4 * rr + (lane >> 4);
+        const float4 lo = *reinterpret_cast<const float4*>(&E[row * EP + col]);
+        const float4 hi = *reinterpret_cast<const float4*>(&E[row * EP + col + 4]);
+        const uint32_t xw[4] = {xv[rr].x, xv[rr].y, xv[rr].z, xv[rr].w};
+        const float a[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        uint32_t yw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          yw[j] = pack_bf16x2(fmaxf(a[2 * j], 0.0f) * bf16_lo(xw[j]), fmaxf(a[2 * j + 1], 0.0f) * bf16_hi(xw[j]));
         if (m0 + 64 * w + mi * 16 + row < g.M)
-          *reinterpret_cast<uint2*>(dst[rr]) = make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
+          *reinterpret_cast<uint4*>(dst[rr]) = make_uint4(yw[0], yw[1], yw[2], yw[3]);
       }
       __syncthreads();
     }
     return;
   }
 
-  // X with q: a lane's columns are the same in every call of the epilogue
-  // (4 (lane & 31) .. + 3: pairs (n, n+1), (n+2, n+3)), so their two
-  // frequencies are loaded once per tile, not once per call.
-  float fq[2] = {0.0f, 0.0f};
-  if (KIND == G_X && g.q) {
-    const int64_t n0 = c0 + 4 * (lane & 31) - h * g.N;
-    fq[0] = g.freqs[n0];
-    fq[1] = g.freqs[n0 + 2];
+  if (KIND == G_X) {
+    // x = ReLU(acc) and q = rope(x): 8 columns per lane and call, one 16-byte
+    // streaming store each (GBs at C5, read back only by later launches).  A
+    // lane's columns (pairs (n, n+1) .. (n+6, n+7)) are the same in every
+    // call, so their frequencies are loaded once per tile.
+    float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (g.q) {
+      const int64_t n0 = c0 + 8 * (lane & 15) - h * g.N;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fq[j] = g.freqs[n0 + 2 * j];
+    }
+    epilogue8_64x128(acc, lds, w, lane, [&](int row, int col, float4 lo, float4 hi) {
+      const int64_t m = m0 + 64 * w + row, c = c0 + col;
+      if (m >= g.M) return;
+      const int64_t bb = m / g.T, t = m - bb * g.T, n = c - h * g.N;
+      const int64_t o = ((bb * g.H + h) * g.T + t) * g.N + n;
+      const float r[8] = {fmaxf(lo.x, 0.0f), fmaxf(lo.y, 0.0f), fmaxf(lo.z, 0.0f), fmaxf(lo.w, 0.0f),
+                          fmaxf(hi.x, 0.0f), fmaxf(hi.y, 0.0f), fmaxf(hi.z, 0.0f), fmaxf(hi.w, 0.0f)};
+      __builtin_nontemporal_store(u32x4{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]),
+                                        pack_bf16x2(r[4], r[5]), pack_bf16x2(r[6], r[7])},
+                                  reinterpret_cast<u32x4*>(g.xy + o));
+      if (g.xf) {
+        *reinterpret_cast<float4*>(g.xf + o) = make_float4(r[0], r[1], r[2], r[3]);
+        *reinterpret_cast<float4*>(g.xf + o + 4) = make_float4(r[4], r[5], r[6], r[7]);
+      }
+      if (g.q) {
+        // Phase frac(p f) in the reference's f32 op order, cos / sin by
+        // v_cos_f32 / v_sin_f32 (argument in revolutions); the rotation in
+        // the op order of attention.rs:488-501.
+        const float p = (float)(g.fixed ? g.pos0 : g.pos0 + t);
+        float qv[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float fr = rope_frac(p, fq[j]);
+          rope_pair_exact(r[2 * j], r[2 * j + 1], __builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr),
+                          qv[2 * j], qv[2 * j + 1]);
+        }
+        __builtin_nontemporal_store(u32x4{pack_bf16x2(qv[0], qv[1]), pack_bf16x2(qv[2], qv[3]),
+                                          pack_bf16x2(qv[4], qv[5]), pack_bf16x2(qv[6], qv[7])},
+                                    reinterpret_cast<u32x4*>(g.q + o));
+      }
+    });
+    return;
   }
+
   epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
     const int64_t m = m0 + 64 * w + row, c = c0 + col;
     if (m >= g.M) return;
@@ -161,41 +203,15 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
       if (c < g.D) *reinterpret_cast<float4*>(&g.zpart[((int64_t)kp * g.M + m) * g.D + c]) = v;
       return;
     }
-    if (KIND == G_L) {
-      float* dst = g.zpart + m * g.V + c;
-      if (c + 3 < g.V && (g.V & 3) == 0) {
-        *reinterpret_cast<float4*>(dst) = v;
-      } else {
-        const float e[4] = {v.x, v.y, v.z, v.w};
+    // KIND == G_L: logits
+    float* dst = g.zpart + m * g.V + c;
+    if (c + 3 < g.V && (g.V & 3) == 0) {
+      *reinterpret_cast<float4*>(dst) = v;
+    } else {
+      const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (c + j < g.V) dst[j] = e[j];
-      }
-      return;
-    }
-    const int64_t bb = m / g.T, t = m - bb * g.T, n = c - h * g.N;
-    const int64_t o = ((bb * g.H + h) * g.T + t) * g.N + n;
-    const float r[4] = {fmaxf(v.x, 0.0f), fmaxf(v.y, 0.0f), fmaxf(v.z, 0.0f), fmaxf(v.w, 0.0f)};
-    // Streaming stores for x and q (GBs at C5, read back only by later
-    // launches): GEMM X 1.04 -> 0.98 ms at C5.
-    __builtin_nontemporal_store(u32x2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])},
-                                reinterpret_cast<u32x2*>(g.xy + o));
-    if (g.xf) *reinterpret_cast<float4*>(g.xf + o) = make_float4(r[0], r[1], r[2], r[3]);
-    if (g.q) {
-      // q = rope(x) from the f32 activations: pairs (n, n+1), (n+2, n+3);
-      // phase frac(p f) in the reference's f32 op order, cos / sin by
-      // v_cos_f32 / v_sin_f32 (argument in revolutions); the rotation in
-      // the op order of attention.rs:488-501.
-      const float p = (float)(g.fixed ? g.pos0 : g.pos0 + t);
-      float qv[4];
-#pragma unroll
-      for (int j = 0; j < 4; j += 2) {
-        const float fr = rope_frac(p, fq[j / 2]);
-        rope_pair_exact(r[j], r[j + 1], __builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr),
-                        qv[j], qv[j + 1]);
-      }
-      __builtin_nontemporal_store(u32x2{pack_bf16x2(qv[0], qv[1]), pack_bf16x2(qv[2], qv[3])},
-                                  reinterpret_cast<u32x2*>(g.q + o));
+      for (int j = 0; j < 4; ++j)
+        if (c + j < g.V) dst[j] = e[j];
     }
   });
 }
