@@ -38,9 +38,11 @@ SEED = 20260729
 # profiles/prefill_c2_traffic.txt, profiles/decode_c3_traffic.txt,
 # profiles/long_prefill_c4_traffic.txt.  Counters cannot run inside this
 # process, so the figures are recorded here; they change when the kernels do.
-TRAFFIC_PREFILL_C2 = 1429.6e6   # one prefill_mfma_kernel launch (the pass: 1497.3e6)
-TRAFFIC_DECODE_C3 = 428.0e6     # one decode_kernel launch
-TRAFFIC_LONG_C4 = 4475.2e6      # the 16 prefill_mfma_kernel launches of one C4 call (the call: 5721.0e6)
+TRAFFIC_PREFILL_C2 = 1429.6e6       # one prefill_mfma_kernel launch
+TRAFFIC_PREFILL_C2_PASS = 1497.3e6  # the whole C2 pass (prep, prefill, ctx)
+TRAFFIC_DECODE_C3 = 428.0e6         # one decode_kernel launch
+TRAFFIC_LONG_C4 = 4475.2e6          # the 16 prefill_mfma_kernel launches of one C4 call
+TRAFFIC_LONG_C4_CALL = 5721.0e6     # the whole C4 call
 
 
 def parse():
@@ -185,7 +187,7 @@ def bench_prefill(torch, args):
                      "kernel_avg_us": round(k_ms / k_n * 1e3, 2), "flop_per_launch": k_flop / k_n,
                      "pass": {"kernels": "prep_bf16_kernel + prefill_mfma_kernel + ctx_kernel",
                               "event_ms": round(ev_ms, 4), "tflops": round(pass_tflops, 2),
-                              "flop": flop, "traffic": 1467.0e6}},
+                              "flop": flop, "traffic": TRAFFIC_PREFILL_C2_PASS}},
         "shape": {"B": B, "nh": H, "T": T, "N": N, "D": D, "chunk": C},
     }
 
@@ -234,7 +236,7 @@ def bench_long(torch, args):
                          "traffic": TRAFFIC_LONG_C4,
                          "kernel": f"prefill_mfma_kernel, {k_n:.0f} launches per call (summed)",
                          "kernel_ms_per_call": round(k_ms, 4), "flop_per_call": k_flop,
-                         "call": {"tflops": round(call_tflops, 2), "flop": flop, "traffic": 5682.3e6}}}
+                         "call": {"tflops": round(call_tflops, 2), "flop": flop, "traffic": TRAFFIC_LONG_C4_CALL}}}
 
 
 def bench_decode(torch, args):
