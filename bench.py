@@ -10,7 +10,7 @@ Also reported (``decode``): BASELINE config 3, 256 decode steps of B=64
 streams after a 1024-token prefill, fp32 rho, tokens/s = B / step time, with
 its HBM roofline.
 
-Roofline (algorithmic work):
+Roofline (algorithmic work; the bound kernel is timed live with HIP events):
   prefill FLOP/step = B*nh*T*(4*N*D + (C-1)*(N+D))          vs 2.5 PFLOP/s bf16
   decode  bytes/step = sum_streams (4N + 4D + 2*|A|*4D + 4D)  vs 8 TB/s HBM
 with |A| the exact active-row count of each stream at that step.
@@ -520,7 +520,8 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the recurrent-attention path on a "
-              "single MI355X (streams shard across GPUs with no exchange; see DESIGN.md). "
+              "single MI355X (the (batch, head) streams are independent, so N GPUs would each run "
+              "B*nh/N of them with no exchange). "
               "Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
