@@ -271,7 +271,8 @@ def bench_decode(torch, args):
         rope.pos0 = P + i
         st = lib.bdh_decode_step(B, H, 1, N, D, ctypes.c_void_p(xs[i].data_ptr()),
                                  ctypes.c_void_p(vs[i].data_ptr()), ctypes.c_void_p(rho.data_ptr()),
-                                 ctypes.byref(rope), ctypes.c_void_p(a.data_ptr()), None, None, stream)
+                                 None, ctypes.byref(rope), ctypes.c_void_p(a.data_ptr()), None, None,
+                                 stream)
         if st != 0:
             raise RuntimeError(f"decode failed: {_lib.last_error()}")
 

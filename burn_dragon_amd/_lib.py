@@ -60,8 +60,8 @@ SIGNATURES = {
     "bdh_recurrent_attention_rope_fwd": (_i32, [ctypes.POINTER(BdhRecurrentPlan), _i32, _vp, _vp,
                                                 _vp, _vp, ctypes.POINTER(BdhRope), _vp, _vp, _i32,
                                                 _vp]),
-    "bdh_decode_step": (_i32, [_i64] * 5 + [_vp, _vp, _vp, ctypes.POINTER(BdhRope), _vp, _vp, _vp,
-                                            _vp]),
+    "bdh_decode_step": (_i32, [_i64] * 5 + [_vp, _vp, _vp, _vp, ctypes.POINTER(BdhRope), _vp,
+                                            _vp, _vp, _vp]),
     "bdh_dense_causal_attention_fwd": (_i32, [ctypes.POINTER(BdhRecurrentPlan), _i32, _vp, _vp,
                                               _vp, _vp, _vp]),
     "bdh_lowrank_pack_weights": (_i32, [_i64] * 3 + [_vp] * 7),
@@ -76,6 +76,7 @@ SIGNATURES = {
     "bdh_profile_kernel_timing": (_i32, [_i32]),
     "bdh_profile_kernel_get": (_i32, [_i32, ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_int64)]),
+    "bdh_scratch_release": (_i32, [_vp]),
     "bdh_last_error": (ctypes.c_char_p, []),
     "bdh_version": (ctypes.c_char_p, []),
 }

@@ -29,40 +29,90 @@ bdh_status hip_fail(hipError_t e, const char* what) {
 }
 
 // --------------------------------------------------------------- scratch ----
+// Scratch is kept per (device, stream): calls on different streams never
+// share a buffer, so they may run concurrently.  A slot grows (by 1.25x) on
+// the first call that needs more.  Growth is refused while the stream is
+// being captured into a graph (a graph must only hold buffers that outlive
+// it: run the largest shape once eagerly on the capturing stream first).
+// A replaced buffer is freed once this stream's queued work is done, unless
+// a graph was ever captured on the stream with this set: a graph keeps its
+// buffer pointers, so the buffer then stays until bdh_scratch_release.
 namespace {
-struct DeviceScratch {
+struct ScratchSet {
   void* ptr[SLOT_COUNT] = {};
   size_t bytes[SLOT_COUNT] = {};
-  std::map<std::pair<int64_t, uint32_t>, float*> freqs;
+  bool captured = false;
+  std::vector<void*> retired;
 };
 std::mutex g_scratch_mu;
-std::map<int, DeviceScratch> g_scratch;
+std::map<std::pair<int, hipStream_t>, ScratchSet> g_sets;
+std::map<int, std::map<std::pair<int64_t, uint32_t>, float*>> g_freqs;
 
-DeviceScratch& device_scratch(int dev) { return g_scratch[dev]; }
+// Counters of the entry point running on this thread (profile snapshot).
+struct CallCounters {
+  uint64_t allocations = 0, upload_bytes = 0, reuse_hits = 0, reuse_bytes = 0;
+};
+thread_local CallCounters t_call;
 }  // namespace
 
-bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc) {
+bdh_status stream_capturing(hipStream_t st, bool* capturing) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(st, &cs);
+  // An implicit capture error (the legacy stream queried while another
+  // stream captures) counts as capturing.
+  *capturing = e != hipSuccess || cs != hipStreamCaptureStatusNone;
+  if (e != hipSuccess) (void)hipGetLastError();
+  return BDH_OK;
+}
+
+bdh_status scratch(hipStream_t st, int slot, size_t bytes, void** out, bool zero_on_alloc) {
   int dev = 0;
   BDH_HIP_TRY(hipGetDevice(&dev));
+  bool capturing = false;
+  stream_capturing(st, &capturing);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  DeviceScratch& ds = device_scratch(dev);
+  ScratchSet& ss = g_sets[{dev, st}];
+  if (capturing) ss.captured = true;
   if (bytes == 0) bytes = 256;
-  if (ds.bytes[slot] < bytes) {
-    if (ds.ptr[slot]) {
-      // Work already queued may still use the old buffer.
-      BDH_HIP_TRY(hipDeviceSynchronize());
-      BDH_HIP_TRY(hipFree(ds.ptr[slot]));
-      ds.ptr[slot] = nullptr;
-      ds.bytes[slot] = 0;
+  if (ss.bytes[slot] < bytes) {
+    if (capturing)
+      return fail(BDH_UNSUPPORTED,
+                  "scratch must grow, which cannot happen during graph capture: run this shape "
+                  "once eagerly on the capturing stream before capturing");
+    if (ss.ptr[slot]) {
+      if (ss.captured) {
+        ss.retired.push_back(ss.ptr[slot]);
+      } else {
+        // Work queued on this stream may still use the old buffer.
+        BDH_HIP_TRY(hipStreamSynchronize(st));
+        BDH_HIP_TRY(hipFree(ss.ptr[slot]));
+      }
+      ss.ptr[slot] = nullptr;
+      ss.bytes[slot] = 0;
     }
     const size_t grow = bytes + bytes / 4;
     void* p = nullptr;
     BDH_HIP_TRY(hipMalloc(&p, grow));
-    if (zero_on_alloc) BDH_HIP_TRY(hipMemset(p, 0, grow));
-    ds.ptr[slot] = p;
-    ds.bytes[slot] = grow;
+    ++t_call.allocations;
+    if (zero_on_alloc) BDH_HIP_TRY(hipMemsetAsync(p, 0, grow, st));
+    ss.ptr[slot] = p;
+    ss.bytes[slot] = grow;
   }
-  *out = ds.ptr[slot];
+  *out = ss.ptr[slot];
+  return BDH_OK;
+}
+
+bdh_status scratch_release(hipStream_t st) {
+  int dev = 0;
+  BDH_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_sets.find({dev, st});
+  if (it == g_sets.end()) return BDH_OK;
+  BDH_HIP_TRY(hipStreamSynchronize(st));
+  for (int i = 0; i < SLOT_COUNT; ++i)
+    if (it->second.ptr[i]) BDH_HIP_TRY(hipFree(it->second.ptr[i]));
+  for (void* p : it->second.retired) BDH_HIP_TRY(hipFree(p));
+  g_sets.erase(it);
   return BDH_OK;
 }
 
@@ -79,27 +129,37 @@ void rope_freqs_host(int64_t latent, float theta, float* out) {
   }
 }
 
-bdh_status rope_freqs_device(int64_t latent, float theta, const float** out) {
+// Device copy of the table, one per (device, latent, theta), shared by all
+// streams (read-only once written).  The upload is synchronous and happens
+// once per key; it is refused during graph capture.
+bdh_status rope_freqs_device(int64_t latent, float theta, hipStream_t st, const float** out) {
   int dev = 0;
   BDH_HIP_TRY(hipGetDevice(&dev));
   uint32_t tbits;
   memcpy(&tbits, &theta, 4);
-  {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    auto& m = device_scratch(dev).freqs;
-    auto it = m.find({latent, tbits});
-    if (it != m.end()) {
-      *out = it->second;
-      return BDH_OK;
-    }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto& m = g_freqs[dev];
+  auto it = m.find({latent, tbits});
+  if (it != m.end()) {
+    ++t_call.reuse_hits;
+    t_call.reuse_bytes += sizeof(float) * (uint64_t)latent;
+    *out = it->second;
+    return BDH_OK;
   }
+  bool capturing = false;
+  stream_capturing(st, &capturing);
+  if (capturing)
+    return fail(BDH_UNSUPPORTED,
+                "the RoPE frequency table of this (latent, theta) is uploaded on first use, which "
+                "cannot happen during graph capture: run one eager call first");
   std::vector<float> host((size_t)latent);
   rope_freqs_host(latent, theta, host.data());
   float* d = nullptr;
   BDH_HIP_TRY(hipMalloc(&d, sizeof(float) * (size_t)latent));
+  ++t_call.allocations;
   BDH_HIP_TRY(hipMemcpy(d, host.data(), sizeof(float) * (size_t)latent, hipMemcpyHostToDevice));
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  device_scratch(dev).freqs[{latent, tbits}] = d;
+  t_call.upload_bytes += sizeof(float) * (uint64_t)latent;
+  m[{latent, tbits}] = d;
   *out = d;
   return BDH_OK;
 }
@@ -115,10 +175,27 @@ bool prof_env() {
 }
 bool g_prof_on = prof_env();
 
+// One entry-point call.  The fields follow KernelProfileSnapshot
+// (profiling.rs:3-16) as recurrent.rs:206-215, 344-356 fills them, with this
+// library's meaning of each:
+//   setup_ns      validation, plan and table lookup before the first launch;
+//   copy_ns       host time of separate rho copies (none: the private copy of
+//                 the reference, recurrent.rs:259, is fused into the kernel
+//                 that writes rho_out), so it stays 0;
+//   transient_allocations  device buffers allocated by the call (scratch
+//                 growth, a first-use table); 0 once a shape is warm, where
+//                 the reference allocates 5 per call;
+//   metadata_upload_bytes  host-to-device bytes of shape tables (the RoPE
+//                 frequencies on first use; plans upload nothing);
+//   metadata_reuse_hits / _bytes  calls that found their table resident;
+//   resident_rollout_steps  T = 1 steps that updated rho in place through
+//                 the sparse decode (the state never left HBM).
 struct ProfScope {
   std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
   uint64_t launches = 0;
   uint64_t setup_ns = 0;
+  uint64_t rollout_steps = 0;
+  ProfScope() { t_call = CallCounters{}; }
   void done(bool ok) {
     if (!g_prof_on) return;
     const auto ns = (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
@@ -129,6 +206,11 @@ struct ProfScope {
     g_prof.total_ns += ns;
     g_prof.setup_ns += setup_ns;
     g_prof.dispatch_ns += ns > setup_ns ? ns - setup_ns : 0;
+    g_prof.transient_allocations += t_call.allocations;
+    g_prof.metadata_upload_bytes += t_call.upload_bytes;
+    g_prof.metadata_reuse_hits += t_call.reuse_hits;
+    g_prof.metadata_reuse_bytes += t_call.reuse_bytes;
+    g_prof.resident_rollout_steps += rollout_steps;
   }
 };
 }  // namespace
@@ -233,17 +315,43 @@ bdh_status forward_common(const bdh_recurrent_plan* plan, int32_t dtype, const v
 
   const float* freqs = nullptr;
   if (rope) {
-    st = rope_freqs_device(N, rope->theta, &freqs);
+    st = rope_freqs_device(N, rope->theta, hs, &freqs);
     if (st != BDH_OK) return st;
   }
   prof.setup_ns = (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
                       std::chrono::steady_clock::now() - prof.t0).count();
 
+  // One token: the reference picks its kernel by T (forward_runtime.rs:
+  // 235-256) and decodes through this same op (sequence_dispatch.rs:109-124).
+  // fp32 runs the one-token step: the sparse row gather when rho is updated
+  // in place without decay, otherwise one dense pass that writes every row
+  // of rho_out (the private copy fused with the update).
+  if (T == 1 && dtype == BDH_F32 && want_rho) {
+    DecodeArgs d;
+    d.x = (const float*)q;
+    d.v = (const float*)v;
+    d.rho_in = rho_in;
+    d.rho = rho_out;
+    d.decay = decay;
+    d.freqs = freqs;
+    d.pos = rope ? (float)rope->pos0 : 0.0f;
+    d.a_out = ctx;
+    d.idx_out = nullptr;
+    d.cnt_out = nullptr;
+    d.B = B; d.H = H; d.Hv = Hv; d.N = N; d.D = D;
+    if (N > (int64_t)1 << 24) return fail(BDH_UNSUPPORTED, "latent too large for the one-token step");
+    st = run_decode(d, hs, &prof.launches);
+    if (st != BDH_OK) return st;
+    if (rho_in && rho_in == rho_out && !decay) prof.rollout_steps = 1;
+    prof.done(true);
+    return BDH_OK;
+  }
+
   if (dtype == BDH_F32) {
     const float* qr = (const float*)q;
     if (rope) {
       void* rot = nullptr;
-      st = scratch(SLOT_ROTATED, (size_t)(B * H * T * N) * sizeof(float), &rot);
+      st = scratch(hs, SLOT_ROTATED, (size_t)(B * H * T * N) * sizeof(float), &rot);
       if (st != BDH_OK) return st;
       BDH_HIP_TRY(launch_rope_rotate_f32((const float*)q, freqs, (float*)rot, B * H, T, N,
                                          rope->pos0, rope->mode == BDH_ROPE_FIXED, hs));
@@ -252,7 +360,7 @@ bdh_status forward_common(const bdh_recurrent_plan* plan, int32_t dtype, const v
     }
     const int64_t Lmax = want_rho ? (T < 256 ? T : 256) : T;
     void* scores = nullptr;
-    st = scratch(SLOT_SCORES, (size_t)(B * H * Lmax * Lmax) * sizeof(float), &scores);
+    st = scratch(hs, SLOT_SCORES, (size_t)(B * H * Lmax * Lmax) * sizeof(float), &scores);
     if (st != BDH_OK) return st;
     F32Args a{qr, (const float*)v, want_rho ? rho_in : nullptr, decay, ctx, rho_out,
               (float*)scores, B, H, Hv, T, N, D, Lmax, want_rho};
@@ -306,10 +414,6 @@ bdh_status bdh_recurrent_plan_new(int64_t batch, int64_t heads, int64_t value_he
   bdh_status st = check_plan(&p);
   if (st != BDH_OK) return st;
   *out = p;
-  if (g_prof_on) {
-    std::lock_guard<std::mutex> lock(g_prof_mu);
-    g_prof.metadata_reuse_hits += 0;
-  }
   return BDH_OK;
 }
 
@@ -351,28 +455,34 @@ bdh_status bdh_dense_causal_attention_fwd(const bdh_recurrent_plan* plan, int32_
 
 bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads, int64_t latent,
                            int64_t embd, const float* x, const float* value, float* rho,
-                           const bdh_rope* rope, float* a_out, int32_t* active_idx_out,
-                           int32_t* active_cnt_out, void* stream) {
+                           const float* decay, const bdh_rope* rope, float* a_out,
+                           int32_t* active_idx_out, int32_t* active_cnt_out, void* stream) {
   ProfScope prof;
   bdh_recurrent_plan p{batch, heads, value_heads, 1, latent, embd};
   bdh_status st = check_plan(&p);
   if (st != BDH_OK) return st;
   if (!x || !value || !rho || !a_out) return fail(BDH_EINVAL, "null tensor pointer");
+  for (const void* t : {(const void*)x, (const void*)value, (const void*)rho, (const void*)decay,
+                        (const void*)a_out, (const void*)active_idx_out, (const void*)active_cnt_out})
+    if (((uintptr_t)t & 3) != 0) return fail(BDH_EINVAL, "tensor pointers must be 4-byte aligned");
   if (latent > (int64_t)1 << 24) return fail(BDH_UNSUPPORTED, "latent too large");
+  if (rope && rope->mode != BDH_ROPE_SEQUENTIAL && rope->mode != BDH_ROPE_FIXED)
+    return fail(BDH_EINVAL, "unknown rope mode");
   if (rope && latent % 2 != 0) return fail(BDH_UNSUPPORTED, "RoPE needs an even latent");
   if (rope && (rope->pos0 < 0 || rope->pos0 >= (int64_t)1 << 24))
     return fail(BDH_UNSUPPORTED, "position must lie in [0, 2^24)");
   if (rope && !(rope->theta > 0.0f)) return fail(BDH_EINVAL, "rope theta must be > 0");
-  if (embd > 2048) return fail(BDH_UNSUPPORTED, "decode step needs embd <= 2048");
   const float* freqs = nullptr;
   if (rope) {
-    st = rope_freqs_device(latent, rope->theta, &freqs);
+    st = rope_freqs_device(latent, rope->theta, (hipStream_t)stream, &freqs);
     if (st != BDH_OK) return st;
   }
   DecodeArgs a;
   a.x = x;
   a.v = value;
+  a.rho_in = rho;
   a.rho = rho;
+  a.decay = decay;
   a.freqs = freqs;
   a.pos = rope ? (float)rope->pos0 : 0.0f;
   a.a_out = a_out;
@@ -384,9 +494,13 @@ bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads, in
   a.N = latent;
   a.D = embd;
   st = run_decode(a, (hipStream_t)stream, &prof.launches);
-  if (st == BDH_OK) prof.done(true);
-  return st;
+  if (st != BDH_OK) return st;
+  if (!decay) prof.rollout_steps = 1;
+  prof.done(true);
+  return BDH_OK;
 }
+
+bdh_status bdh_scratch_release(void* stream) { return scratch_release((hipStream_t)stream); }
 
 bdh_status bdh_lowrank_pack_weights(int64_t heads, int64_t latent, int64_t embd,
                                     const float* encoder, const float* encoder_v,
@@ -435,7 +549,7 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
     return fail(BDH_UNSUPPORTED, "layer too large for one launch");
   const float* freqs = nullptr;
   if (rope) {
-    st = rope_freqs_device(p.latent, rope->theta, &freqs);
+    st = rope_freqs_device(p.latent, rope->theta, (hipStream_t)stream, &freqs);
     if (st != BDH_OK) return st;
   }
   LayerArgs a;

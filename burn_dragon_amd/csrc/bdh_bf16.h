@@ -114,6 +114,17 @@ __device__ __forceinline__ float decay_pow(const float* decay, int64_t h, float 
   return decay ? powf(decay[h], e) : 1.0f;
 }
 
+// d^e for an integer e >= 0, as the reference's repeated products give it
+// (recurrent.rs:415): 1 at e = 0 (d = 0 included), exp2(e log2 |d|)
+// otherwise, negated for d < 0 and odd e.  l2a = log2|d| (-inf for d = 0,
+// where exp2 gives the 0 of 0^e, e > 0).
+__device__ __forceinline__ float decay_log2(float d) { return log2f(fabsf(d)); }
+__device__ __forceinline__ float decay_pow_int(float d, float l2a, int e) {
+  if (e == 0) return 1.0f;
+  const float m = exp2f((float)e * l2a);
+  return (d < 0.0f && (e & 1)) ? -m : m;
+}
+
 // --- launch interface of the gram + state kernel (mfma_prefill.hip) --------
 // One launch runs up to three kinds of work unit, heaviest first:
 //   gram units  (stream, N range kp, interval iv, 256-row x 128-column tile

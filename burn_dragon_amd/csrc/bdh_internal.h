@@ -43,7 +43,14 @@ enum ScratchSlot {
   SLOT_DECODE_CNT,   // decode range active counts   [S, G] int32
   SLOT_COUNT
 };
-bdh_status scratch(int slot, size_t bytes, void** out, bool zero_on_alloc = false);
+// Scratch of the calling stream (see api.hip): grows on first use of a
+// larger shape, refused (BDH_UNSUPPORTED) while the stream is capturing.
+bdh_status scratch(hipStream_t st, int slot, size_t bytes, void** out, bool zero_on_alloc = false);
+// Frees the scratch kept for `st` on the current device (after the stream's
+// queued work), including buffers retired while a graph held them.
+bdh_status scratch_release(hipStream_t st);
+// True when `st` is being captured into a graph.
+bdh_status stream_capturing(hipStream_t st, bool* capturing);
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus();
@@ -54,8 +61,9 @@ int device_cus();
 int ktime_begin(int kind, hipStream_t st);
 void ktime_end(int handle, hipStream_t st);
 
-// Device copy of the RoPE frequency table for (latent, theta), cached.
-bdh_status rope_freqs_device(int64_t latent, float theta, const float** out);
+// Device copy of the RoPE frequency table for (latent, theta), cached per
+// device; the first use uploads it (refused during capture of `st`).
+bdh_status rope_freqs_device(int64_t latent, float theta, hipStream_t st, const float** out);
 // Host computation of the same table (attention.rs:552-576).
 void rope_freqs_host(int64_t latent, float theta, float* out);
 
@@ -123,17 +131,29 @@ bdh_status lm_logits(const float* hidden, int64_t M, int64_t D, const bf16_t* he
                      float* logits, hipStream_t st);
 
 // --- decode (decode.hip) ------------------------------------------------------
+// One token per stream (T = 1).  rho_in == rho (not null) and no decay:
+// the sparse step (only the active rows are read and written).  Otherwise
+// the dense step: every row of rho_in (zeros when null) is read and written
+// to rho, rho = (rho_in + rot(x)^T v) * decay, in place or not.
 struct DecodeArgs {
   const float* x;       // [S, N]
   const float* v;       // [B, Hv, D]
-  float* rho;           // [S, N, D]
+  const float* rho_in;  // [S, N, D] or null (zeros)
+  float* rho;           // [S, N, D] successor state
+  const float* decay;   // [H] or null (ones)
   const float* freqs;   // null -> x already rotated
   float pos;
   float* a_out;         // [S, D]
   int32_t* idx_out;     // [S, N] or null
   int32_t* cnt_out;     // [S] or null
   int64_t B, H, Hv, N, D;
+  // Buffers for the range readouts and lists of a split stream; null: the
+  // stream's scratch.
+  void* part_buf = nullptr;
+  size_t part_bytes = 0;
 };
 bdh_status run_decode(const DecodeArgs& a, hipStream_t st, uint64_t* launches);
+// Bytes of range buffers run_decode needs for a.
+size_t decode_part_bytes(const DecodeArgs& a);
 
 }  // namespace bdh

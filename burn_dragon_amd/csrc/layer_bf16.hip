@@ -607,7 +607,7 @@ bdh_status pack_lm_head(int64_t D, int64_t V, const float* head, bf16_t* packed,
 bdh_status lm_logits(const float* hidden, int64_t M, int64_t D, const bf16_t* head, int64_t V,
                      float* logits, hipStream_t st) {
   void* hb = nullptr;
-  bdh_status s = scratch(SLOT_LAYER_CUR, (size_t)(M * D) * sizeof(bf16_t), &hb);
+  bdh_status s = scratch(st, SLOT_LAYER_CUR, (size_t)(M * D) * sizeof(bf16_t), &hb);
   if (s != BDH_OK) return s;
   hipLaunchKernelGGL(to_bf16_kernel, dim3(cdiv(M * D, 1024)), dim3(256), 0, st, hidden,
                      (bf16_t*)hb, M * D);
@@ -645,32 +645,32 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
       if (tiles_z * cand >= 512) break;
     }
   }
-  bdh_status s = scratch(SLOT_LAYER_CUR, (size_t)(M * a.D) * sizeof(bf16_t), &curb);
+  bdh_status s = scratch(st, SLOT_LAYER_CUR, (size_t)(M * a.D) * sizeof(bf16_t), &curb);
   if (s != BDH_OK) return s;
-  s = scratch(SLOT_LAYER_XY, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xy);
+  s = scratch(st, SLOT_LAYER_XY, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xy);
   if (s != BDH_OK) return s;
   // q: rope(x) in bf16 for the MFMA attention, or x in f32 for the decode
   // step (which rotates as it gathers).
   void* q = nullptr;
   if (decode) {
-    s = scratch(SLOT_LAYER_Q, (size_t)(S * a.N) * sizeof(float), &q);
+    s = scratch(st, SLOT_LAYER_Q, (size_t)(S * a.N) * sizeof(float), &q);
     if (s != BDH_OK) return s;
   } else if (a.freqs) {
-    s = scratch(SLOT_LAYER_Q, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &q);
+    s = scratch(st, SLOT_LAYER_Q, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &q);
     if (s != BDH_OK) return s;
   }
-  s = scratch(SLOT_LAYER_ATTN, (size_t)(S * a.T * a.D) * sizeof(float), &attn);
+  s = scratch(st, SLOT_LAYER_ATTN, (size_t)(S * a.T * a.D) * sizeof(float), &attn);
   if (s != BDH_OK) return s;
-  s = scratch(SLOT_LAYER_AN, (size_t)(S * a.T * a.D) * sizeof(bf16_t), &an);
+  s = scratch(st, SLOT_LAYER_AN, (size_t)(S * a.T * a.D) * sizeof(bf16_t), &an);
   if (s != BDH_OK) return s;
-  s = scratch(SLOT_LAYER_Z, (size_t)(ks * M * a.D) * sizeof(float), &zp);
+  s = scratch(st, SLOT_LAYER_Z, (size_t)(ks * M * a.D) * sizeof(float), &zp);
   if (s != BDH_OK) return s;
   // A carried state whose successor is not kept still needs the state path
   // (readout of rho_in); its rho goes to scratch.
   float* rho_out = a.rho_out;
   if (!decode && a.rho_in && !rho_out) {
     void* r = nullptr;
-    s = scratch(SLOT_LAYER_RHO, (size_t)(S * a.N * a.D) * sizeof(float), &r);
+    s = scratch(st, SLOT_LAYER_RHO, (size_t)(S * a.N * a.D) * sizeof(float), &r);
     if (s != BDH_OK) return s;
     rho_out = (float*)r;
   }
@@ -702,7 +702,9 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
     DecodeArgs d;
     d.x = (const float*)q;
     d.v = a.cur;
+    d.rho_in = a.rho_out;
     d.rho = a.rho_out;
+    d.decay = nullptr;
     d.freqs = a.freqs;
     d.pos = (float)a.pos0;
     d.a_out = (float*)attn;

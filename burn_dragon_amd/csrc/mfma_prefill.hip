@@ -112,7 +112,8 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   // Scores of rows ti < Lc and columns tj < Lc: times d^(ti - tj) below
   // the diagonal, 0 on and above it.  Waves that computed nothing still
   // take part in the epilogue's barriers.
-  const float l2d = DECAY ? log2f(a.decay[s % a.H]) : 0.0f;
+  const float dk = DECAY ? a.decay[s % a.H] : 1.0f;
+  const float l2d = DECAY ? decay_log2(dk) : 0.0f;
   float* P = a.part + (((int64_t)kp * a.S + s) * a.n_iv + iv) * a.Lp * a.Lp;
   epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
     const int64_t ti = wr0 + row, tj = wc0 + col;
@@ -120,7 +121,7 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
     float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      e[j] = tj + j < ti ? (DECAY ? e[j] * exp2f((float)(ti - tj - j) * l2d) : e[j]) : 0.0f;
+      e[j] = tj + j < ti ? (DECAY ? e[j] * decay_pow_int(dk, l2d, (int)(ti - tj - j)) : e[j]) : 0.0f;
     float* dst = P + ti * a.Lp + tj;
     // Streaming stores: the partials are read once, by the context kernel
     // after this launch (C2: 0.369 -> 0.351 ms per prefill).
@@ -148,7 +149,8 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
   const char* X = reinterpret_cast<const char*>(a.x + s * a.T * a.N);
   const char* CS = reinterpret_cast<const char*>(a.cs);
   const char* VT = reinterpret_cast<const char*>(a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp);
-  const float l2d = DECAY ? log2f(a.decay[h]) : 0.0f;  // d^e = exp2(e log2 d)
+  const float dk = DECAY ? a.decay[h] : 1.0f;
+  const float l2d = DECAY ? decay_log2(dk) : 0.0f;
 
   // x loader: lane block of 2 tokens (2 tp, 2 tp + 1) x 8 neurons (8 nv ..).
   // In a unit whose steps run past T (ragged last interval, !WHOLE), tokens
@@ -190,8 +192,8 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
     float w0 = 1.0f, w1 = 1.0f;
     if (DECAY) {
       const int64_t tl = (int64_t)cur * BK + 2 * tp;
-      w0 = tl < Lc ? exp2f((float)(Lc - tl) * l2d) : 0.0f;
-      w1 = tl + 1 < Lc ? exp2f((float)(Lc - tl - 1) * l2d) : 0.0f;
+      w0 = tl < Lc ? decay_pow_int(dk, l2d, (int)(Lc - tl)) : 0.0f;
+      w1 = tl + 1 < Lc ? decay_pow_int(dk, l2d, (int)(Lc - tl - 1)) : 0.0f;
     }
     prep8_f32<ROPE>(st.xr[0], st.cr[0], w0, DECAY, f0);
     prep8_f32<ROPE>(st.xr[1], st.cr[1], w1, DECAY, f1);
@@ -213,7 +215,7 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
 
   // Columns past D (zero v^T rows) are computed and never written; D is a
   // multiple of 32, so a float4 of columns is all in or all out.
-  const float carry = DECAY ? exp2f((float)Lc * l2d) : 1.0f;
+  const float carry = DECAY ? decay_pow_int(dk, l2d, (int)Lc) : 1.0f;
   epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
     const int64_t n = n0 + 64 * wm + row, d = d0 + 128 * wn + col;
     if (d >= a.D) return;
@@ -253,7 +255,8 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
   const float* R = a.rd_rho + s * a.N * a.D;
   const int nk = (int)(a.N / BK);
   const int kb = (int)((int64_t)nk * kp / a.rd_kr), ke = (int)((int64_t)nk * (kp + 1) / a.rd_kr);
-  const float l2d = DECAY ? log2f(a.decay[s % a.H]) : 0.0f;  // d^e = exp2(e log2 d)
+  const float dk = DECAY ? a.decay[s % a.H] : 1.0f;
+  const float l2d = DECAY ? decay_log2(dk) : 0.0f;
 
   // x loader (group g: rows rb + 64 g), as in the gram unit; rows past a
   // ragged interval re-read its last row and are never stored.
@@ -261,7 +264,7 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
   const uint32_t lane_off = (uint32_t)(rb * rowb + kc * 16);
   float wr[4];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) wr[g] = DECAY ? exp2f((float)(r0 + rb + 64 * g) * l2d) : 1.0f;
+  for (int g = 0; g < 4; ++g) wr[g] = DECAY ? decay_pow_int(dk, l2d, (int)(r0 + rb + 64 * g)) : 1.0f;
   // rho loader: lane block of 2 state rows (2 np, 2 np + 1) x 8 columns
   // (8 dv ..); columns past D re-read the last 8 and are never stored.
   const int np = tid & 15, dv = tid >> 4;

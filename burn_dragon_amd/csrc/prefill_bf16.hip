@@ -447,9 +447,9 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   }
 
   void *vt = nullptr, *part = nullptr, *cs = nullptr, *rdp = nullptr, *rho_a = nullptr, *rho_b = nullptr;
-  bdh_status stt = scratch(SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
+  bdh_status stt = scratch(st, SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
   if (stt != BDH_OK) return stt;
-  stt = scratch(SLOT_SCORES, (size_t)(ks * S * n_iv * Lp * Lp) * sizeof(float), &part);
+  stt = scratch(st, SLOT_SCORES, (size_t)(ks * S * n_iv * Lp * Lp) * sizeof(float), &part);
   if (stt != BDH_OK) return stt;
   // With two or more intervals every launch would re-read the RoPE table and
   // re-rotate its x tiles; rotating x once (one read and one write of x)
@@ -457,11 +457,11 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   const bool prerot = a.freqs != nullptr && a.state && n_iv >= 2;
   void* xr = nullptr;
   if (prerot) {
-    stt = scratch(SLOT_ROTATED, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xr);
+    stt = scratch(st, SLOT_ROTATED, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xr);
     if (stt != BDH_OK) return stt;
   } else if (a.freqs) {
     void* tb = nullptr;
-    stt = scratch(SLOT_ROPE_TABLE, TABLE_KEY_WORDS * sizeof(int64_t) + (size_t)(a.T * half) * sizeof(uint32_t),
+    stt = scratch(st, SLOT_ROPE_TABLE, TABLE_KEY_WORDS * sizeof(int64_t) + (size_t)(a.T * half) * sizeof(uint32_t),
                   &tb, true);
     if (stt != BDH_OK) return stt;
     cs = (char*)tb + TABLE_KEY_WORDS * sizeof(int64_t);
@@ -469,14 +469,14 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   if (carried) {
     // Two buffers: interval iv's partials go to buffer iv % 2, and their add
     // runs in the next launch, beside that launch's own readout units.
-    stt = scratch(SLOT_READOUT, (size_t)(2 * rd_kr * S * Lp * a.D) * sizeof(float), &rdp);
+    stt = scratch(st, SLOT_READOUT, (size_t)(2 * rd_kr * S * Lp * a.D) * sizeof(float), &rdp);
     if (stt != BDH_OK) return stt;
   }
   if (a.state && n_iv > 1) {
-    stt = scratch(SLOT_RHO_A, (size_t)(S * a.N * a.D) * sizeof(float), &rho_a);
+    stt = scratch(st, SLOT_RHO_A, (size_t)(S * a.N * a.D) * sizeof(float), &rho_a);
     if (stt != BDH_OK) return stt;
     if (n_iv > 2) {
-      stt = scratch(SLOT_RHO_B, (size_t)(S * a.N * a.D) * sizeof(float), &rho_b);
+      stt = scratch(st, SLOT_RHO_B, (size_t)(S * a.N * a.D) * sizeof(float), &rho_b);
       if (stt != BDH_OK) return stt;
     }
   }

@@ -25,12 +25,15 @@ class DecodeOutput(NamedTuple):
 
 def decode_step(x: torch.Tensor, value: torch.Tensor, rho: torch.Tensor, *,
                 position: Optional[int] = 0, theta: float = DEFAULT_ROPE_THETA,
-                want_active: bool = False, out: Optional[torch.Tensor] = None
-                ) -> Optional[DecodeOutput]:
+                decay: Optional[torch.Tensor] = None, want_active: bool = False,
+                out: Optional[torch.Tensor] = None) -> Optional[DecodeOutput]:
     """x [B,H,N] f32 (unrotated; ``position=None`` means already rotated),
-    value [B,Hv,D] f32, rho [B,H,N,D] f32 updated IN PLACE.  Returns None
-    where the reference would (zero dims, value heads not in {1,H}, non-f32,
-    not on a supported device)."""
+    value [B,Hv,D] f32, rho [B,H,N,D] f32 updated IN PLACE,
+    rho = (rho + rot(x)^T v) * decay.  ``decay`` [H] f32 (ALiBi, exp(-slope):
+    attention.rs:201-208) scales every row, so the step streams all of rho;
+    without it only the active rows are touched.  Returns None where the
+    reference would (zero dims, value heads not in {1,H}, non-f32, not on a
+    supported device)."""
     if not supports_backend():
         return None
     if not (x.is_cuda and value.is_cuda and rho.is_cuda):
@@ -43,6 +46,12 @@ def decode_step(x: torch.Tensor, value: torch.Tensor, rho: torch.Tensor, *,
         return None
     if any(t.dtype != torch.float32 for t in (x, value, rho)):
         return None
+    if decay is not None:
+        # recurrent.rs:247-250: a wrong-shaped decay means ones
+        if not decay.is_cuda or tuple(decay.shape) != (H,):
+            decay = None
+        else:
+            decay = decay.to(torch.float32).contiguous()
     if not rho.is_contiguous():
         raise ValueError("decode_step updates rho in place: it must be contiguous")
     xc = x.contiguous()
@@ -54,7 +63,8 @@ def decode_step(x: torch.Tensor, value: torch.Tensor, rho: torch.Tensor, *,
     if position is not None:
         rope = _lib.BdhRope(_lib.BDH_ROPE_SEQUENTIAL, 0, int(position), float(theta))
     st = _lib.load().bdh_decode_step(
-        B, H, Hv, N, D, _ptr(xc), _ptr(vc), _ptr(rho), ctypes.byref(rope) if rope else None,
+        B, H, Hv, N, D, _ptr(xc), _ptr(vc), _ptr(rho), _ptr(decay),
+        ctypes.byref(rope) if rope else None,
         _ptr(a), _ptr(idx), _ptr(cnt), ctypes.c_void_p(_stream_ptr(x.device)))
     if not _lib.check(st):
         return None

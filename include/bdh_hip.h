@@ -13,12 +13,16 @@
  *   - `stream` is a hipStream_t (NULL = the default stream); launches are
  *     asynchronous on it, nothing synchronises the host;
  *   - the library never allocates or frees caller memory.  It keeps its own
- *     per-device scratch, grown on first use of a shape;
+ *     scratch per (device, stream), grown on the first call of a larger
+ *     shape on that stream.  Growth is refused (BDH_UNSUPPORTED) while the
+ *     stream is being captured into a graph: run the largest shape once
+ *     eagerly on the capturing stream first.  A buffer a captured graph may
+ *     still use is never freed before bdh_scratch_release;
  *   - errors are status codes, never aborts.  BDH_UNSUPPORTED is the
  *     reference's `None` ("use the Burn-op reference instead");
  *     bdh_last_error() gives the message (thread-local).
- *   - calls that share a device's scratch must not overlap on different
- *     streams (one stream per device, as the reference's backend stream).
+ *   - calls on different streams may run concurrently (each stream has its
+ *     own scratch); calls on one stream are ordered by it.
  */
 #ifndef BDH_HIP_H
 #define BDH_HIP_H
@@ -83,6 +87,11 @@ int32_t bdh_supports_backend(void);
  * recurrent.rs:259).  dtype applies to query and value: BDH_F32 runs the
  * fp32 path, BDH_BF16 the MFMA path (fp32 accumulate, fp32 rho/context).
  * chunk: causal block size for the MFMA path (0 = 128).
+ * time == 1 with BDH_F32 (the reference's decode call, sequence_dispatch.rs
+ * :109-124; it selects kernels by T, forward_runtime.rs:235-256) runs the
+ * one-token step of bdh_decode_step: with rho_out == rho_in and no decay
+ * only the active rows of rho are read and written; otherwise one pass
+ * copies every row of rho_in (zeros when NULL) to rho_out with the update.
  * All tensor pointers must be 16-byte aligned (BDH_EINVAL otherwise). */
 bdh_status bdh_recurrent_attention_fwd(const bdh_recurrent_plan* plan, int32_t dtype,
                                        const void* query, const void* value,
@@ -102,21 +111,26 @@ bdh_status bdh_recurrent_attention_rope_fwd(const bdh_recurrent_plan* plan, int3
                                             const bdh_rope* rope, float* context_out,
                                             float* rho_out, int32_t chunk, void* stream);
 
-/* Sparse decode step (T = 1), fp32.  Same result as
- * bdh_recurrent_attention_rope_fwd with time = 1 and decay = NULL, computed
- * by touching only the active rows of rho (RoPE makes them pairs):
+/* Decode step (T = 1), fp32, rho updated in place.  Same result as
+ * bdh_recurrent_attention_rope_fwd with time = 1 and rho_out == rho_in:
  *   A = { i : x_i != 0  or  (x_{i^1} != 0 and frac(pos * f_i) != 0) }
- *   a = rot(x) . rho (read before the update) ;  rho[A] += rot(x)[A]^T v
- * x [B,H,N], value [B,Hv,D], rho [B,H,N,D] updated in place, a_out [B,H,D].
+ *   a = rot(x) . rho (read before the update) ;  rho = (rho + rot(x)^T v) * decay
+ * decay NULL (RoPE models): only the rows in A change, and only they are
+ * read and written (the sparse row gather).  decay [H] f32 (ALiBi, e.g.
+ * exp(-slope), attention.rs:201-208): every row is scaled, so every row is
+ * streamed once (recurrent.rs:415, linear.rs:53-56).
+ * x [B,H,N], value [B,Hv,D], rho [B,H,N,D], a_out [B,H,D].
  * rope NULL: x is already rotated and A = { i : x_i != 0 }.
  * active_idx_out [B,H,N] int32 (ascending, padded with -1) and
  * active_cnt_out [B,H] int32 may be NULL.  This is the per-token call of the
  * reference's decode drivers (dragon.rs:1749-1808, generation.rs:458) through
- * recurrent_attention_with_plan at T = 1. */
+ * recurrent_attention_with_plan at T = 1 (sequence_dispatch.rs:109-124).
+ * Pointers must be 4-byte aligned; 16-byte aligned rows with embd % 4 == 0
+ * take the float4 kernels. */
 bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads,
                            int64_t latent, int64_t embd, const float* x,
-                           const float* value, float* rho, const bdh_rope* rope,
-                           float* a_out, int32_t* active_idx_out,
+                           const float* value, float* rho, const float* decay,
+                           const bdh_rope* rope, float* a_out, int32_t* active_idx_out,
                            int32_t* active_cnt_out, void* stream);
 
 /* Replaces try_fused_dense_causal_attention_wgpu[_with_plan]
@@ -189,9 +203,19 @@ bdh_status bdh_lm_logits(const float* hidden, int64_t rows, int64_t embd,
                          void* stream);
 
 /* Profiling counters with the field names of KernelProfileSnapshot
- * (crates/burn_dragon_kernel/src/profiling.rs:3-16).  Host wall-clock
- * nanoseconds of the entry points; collected only while enabled (the
- * reference's DragonModel_STAGE_PROFILE switch, profiling.rs:50-51). */
+ * (crates/burn_dragon_kernel/src/profiling.rs:3-16), filled per entry-point
+ * call as recurrent.rs:206-215, 344-356 fills them; collected only while
+ * enabled (the reference's DragonModel_STAGE_PROFILE switch,
+ * profiling.rs:50-51).  Host wall-clock nanoseconds: total_ns, setup_ns
+ * (validation and table lookup), dispatch_ns (the rest); copy_ns stays 0
+ * (no separate rho copy: the reference's private copy, recurrent.rs:259, is
+ * fused into the kernel writing rho_out).  transient_allocations: device
+ * buffers the call allocated (scratch growth, a first-use table; 0 once a
+ * shape is warm).  metadata_upload_bytes: host-to-device bytes of tables
+ * (RoPE frequencies on first use; plans upload nothing).
+ * metadata_reuse_hits / _bytes: table lookups that found it resident.
+ * resident_rollout_steps: one-token steps that updated rho in place through
+ * the sparse row gather. */
 typedef struct {
   uint64_t calls, launches;
   uint64_t total_ns, setup_ns, copy_ns, dispatch_ns;
@@ -216,6 +240,12 @@ void bdh_profile_get(bdh_profile_snapshot* out);
 typedef enum { BDH_KERNEL_PREFILL = 0, BDH_KERNEL_DECODE = 1 } bdh_kernel_kind;
 bdh_status bdh_profile_kernel_timing(int32_t enabled);
 bdh_status bdh_profile_kernel_get(int32_t kind, double* total_ms, int64_t* launches);
+
+/* Frees the scratch the library keeps for `stream` on the current device,
+ * after the stream's queued work.  No counterpart in the reference (Burn's
+ * allocator owns its buffers): call it when a stream is retired, and only
+ * after destroying every graph captured on it that calls this library. */
+bdh_status bdh_scratch_release(void* stream);
 
 /* Thread-local message of the last non-OK status of this thread. */
 const char* bdh_last_error(void);

@@ -225,11 +225,11 @@ def lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=0, theta: float = 6
     cur = np.asarray(cur, np.float64)
     enc = np.asarray(encoder, np.float64)
     encv = np.asarray(encoder_v, np.float64)
-    x = np.maximum(np.einsum("btd,hdn->bhtn", cur, enc), 0.0)
+    x = np.maximum(np.matmul(cur[:, None], enc[None]), 0.0)  # [B,H,T,N]
     q = rope_rotate(x.astype(np.float32), pos0=pos0, theta=theta) if pos0 is not None else x
     ctx, rho = recurrent_f64(q, cur[:, None].astype(np.float32), rho0)
     a = layer_norm_f64(ctx)
-    y = x * np.maximum(np.einsum("bhtd,hdn->bhtn", a, encv), 0.0)
+    y = x * np.maximum(np.matmul(a, encv[None]), 0.0)
     mlp = layer_norm_f64(decode_y_neuron_tail_f64(y, decoder))
     return layer_norm_f64(cur + mlp), rho
 

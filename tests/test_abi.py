@@ -87,3 +87,15 @@ def test_forward_rejects_misaligned_pointers_before_any_launch():
                                              ctx, rho, 0, None)
         assert st == _lib.BDH_EINVAL
         assert "aligned" in _lib.last_error()
+
+
+def test_decode_step_rejects_misaligned_pointers_before_any_launch():
+    # The one-token step reads fp32 rows: every pointer must be 4-byte aligned.
+    from burn_dragon_amd import _lib
+    lib = _lib.load()
+    good, bad = 0x10000, 0x10002
+    for x, v, rho, a in ((bad, good, good, good), (good, bad, good, good),
+                         (good, good, bad, good), (good, good, good, bad)):
+        st = lib.bdh_decode_step(1, 2, 1, 16, 8, x, v, rho, None, None, a, None, None, None)
+        assert st == _lib.BDH_EINVAL
+        assert "aligned" in _lib.last_error()

@@ -111,3 +111,45 @@ def test_c4_long_context_full_size(oracle):
     e_rho = rel_l2(host(out.rho), rref)
     print(f"C4 rel-L2 boundaries {e_b:.2e} all {e_all:.2e} rho {e_rho:.2e}")
     assert e_b <= TOL_BF16 and e_all <= TOL_BF16 and e_rho <= TOL_BF16
+
+
+def test_c3_decode_after_1024_token_prefill(oracle):
+    # Config 3 as specified: rho prefilled by a 1024-token synthetic prefill,
+    # then 32 decode steps (positions 1024..1055).  Two sampled streams follow
+    # the oracle step by step from the prefilled state; every stream's rows
+    # outside the step's possible active set stay bit-identical.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    B, H, N, D, P, K = 64, 4, 8192, 256, 1024, 32
+    g = torch.Generator(device="cuda").manual_seed(rc.config_seed(3) + 1)
+    xp = torch.relu(torch.randn(B, H, P, N, generator=g, device="cuda") - 1.645).to(torch.bfloat16)
+    vp = (torch.randn(B, 1, P, D, generator=g, device="cuda") / 16).to(torch.bfloat16)
+    announce("C3 1024-token prefill")
+    pre = bd.try_fused_recurrent_attention_rope(xp, vp, position=0)
+    torch.cuda.synchronize()
+    assert pre is not None
+    del xp, vp
+    rho = pre.rho
+    samples = ((0, 0), (63, 3))
+    ref = {s: host(rho[s[0], s[1]])[None, None].copy() for s in samples}
+    for k in range(K):
+        pos = P + k
+        x = torch.relu(torch.randn(B, H, N, generator=g, device="cuda") - 1.645)
+        v = torch.randn(B, 1, D, generator=g, device="cuda") / 16
+        rho_prev = rho.clone() if k % 8 == 0 else None
+        announce("C3 decode after prefill", pos)
+        out = bd.decode_step(x, v, rho, position=pos)
+        torch.cuda.synchronize()
+        for (b, h) in samples:
+            a_ref, _, _ = oracle.decode_step_f32(host(x[b:b + 1, h:h + 1]), host(v[b:b + 1]),
+                                                 ref[(b, h)], pos)
+            assert rel_l2(host(out.readout[b, h]), a_ref[0, 0]) <= TOL_F32, (k, b, h)
+        if rho_prev is not None:
+            changed = (rho != rho_prev).any(dim=-1)
+            partner = x.view(B, H, N // 2, 2).flip(-1).reshape(B, H, N)
+            assert not bool((changed & ~((x != 0) | (partner != 0))).any()), k
+            del rho_prev
+    for (b, h) in samples:
+        e = rel_l2(host(rho[b, h]), ref[(b, h)][0, 0])
+        print(f"C3 stream ({b},{h}) rho after {K} steps rel-L2 {e:.2e}")
+        assert e <= TOL_F32

@@ -246,3 +246,25 @@ def test_dense_causal_attention_bf16_and_limits(oracle):
     qd = dev(torch, q, torch.bfloat16)
     vd = dev(torch, v, torch.bfloat16)
     assert bd.try_fused_dense_causal_attention(qd, vd, torch.ones(3, device="cuda")) is None
+
+
+@pytest.mark.parametrize("decay", [[0.0, 0.9], [-0.9, 0.5], [-0.5, 0.0]])
+def test_bf16_decay_zero_and_negative(oracle, decay):
+    # Decay powers d^e as repeated products give them (recurrent.rs:415):
+    # d = 0 keeps d^0 = 1 (row 0 of the readout, the carried state at e = 0)
+    # and makes every higher power 0; d < 0 alternates sign.  Two intervals
+    # and a carried state exercise the gram, readout and state units.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(6100 + int(decay[0] * 10))
+    B, H, T, N, D = 1, 2, 640, 512, 64
+    x = oracle.round_bf16(rc.sparse_relu(rng, (B, H, T, N)))
+    v = oracle.round_bf16(rc.gaussian(rng, (B, 1, T, D), 1 / 16))
+    rho0 = rc.gaussian(rng, (B, H, N, D), 0.1)
+    dec = np.array(decay, np.float32)
+    cref, rref = oracle.recurrent_f64(oracle.rope_rotate(x, pos0=2), v, rho0, dec)
+    announce("bf16 decay", decay)
+    ctx, rho = _run(torch, bd, x, v, rho0, dec, torch.bfloat16, rope=(2, False))
+    assert np.isfinite(ctx).all() and np.isfinite(rho).all()
+    assert rel_l2(ctx, cref) <= TOL_BF16
+    assert rel_l2(rho, rref) <= TOL_BF16
