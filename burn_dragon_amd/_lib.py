@@ -62,6 +62,8 @@ SIGNATURES = {
                                                 _vp]),
     "bdh_decode_step": (_i32, [_i64] * 5 + [_vp, _vp, _vp, _vp, ctypes.POINTER(BdhRope), _vp,
                                             _vp, _vp, _vp]),
+    "bdh_decode_step_noalloc": (_i32, [_i64] * 5 + [_vp, _vp, _vp, _vp, ctypes.POINTER(BdhRope),
+                                                    _vp, _vp, _vp, _vp]),
     "bdh_dense_causal_attention_fwd": (_i32, [ctypes.POINTER(BdhRecurrentPlan), _i32, _vp, _vp,
                                               _vp, _vp, _vp]),
     "bdh_lowrank_pack_weights": (_i32, [_i64] * 3 + [_vp] * 7),

@@ -133,6 +133,23 @@ bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads,
                            const bdh_rope* rope, float* a_out, int32_t* active_idx_out,
                            int32_t* active_cnt_out, void* stream);
 
+/* bdh_decode_step without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as bdh_decode_step; its buffers (the RoPE frequency
+ * table and the row-range readouts and lists) live in one 16 MiB device
+ * array per GPU, kept until the process ends.  Limits: latent <= 2^20, and
+ * the range buffers of the shape within 12 MiB (BDH_UNSUPPORTED beyond,
+ * with the reason in bdh_last_error).  Every call on a GPU shares that
+ * GPU's array, so calls that overlap on one GPU (different streams or
+ * threads) race.  The first call with a new (latent, theta) uploads the
+ * frequency table (synchronously on `stream`; refused during capture). */
+bdh_status bdh_decode_step_noalloc(int64_t batch, int64_t heads, int64_t value_heads,
+                                   int64_t latent, int64_t embd, const float* x,
+                                   const float* value, float* rho, const float* decay,
+                                   const bdh_rope* rope, float* a_out, int32_t* active_idx_out,
+                                   int32_t* active_cnt_out, void* stream);
+
 /* Replaces try_fused_dense_causal_attention_wgpu[_with_plan]
  * (crates/burn_dragon_kernel/src/dense_causal_attention.rs:162-261):
  *   ctx = tril(-1)(Q Q^T * decay^(r-c)) V      (no state), decay [H] required.
