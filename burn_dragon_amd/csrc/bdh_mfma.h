@@ -5,6 +5,8 @@
 // that writes the accumulators back as rows through LDS.
 #pragma once
 
+#include <type_traits>
+
 #include "bdh_bf16.h"
 
 namespace bdh {
@@ -130,6 +132,122 @@ __device__ __forceinline__ void run_steps(int kb, int ke, Load&& load, Store&& s
     if (kt + 2 < ke) store(0);
     __syncthreads();
   }
+}
+
+// --- direct global -> LDS loads (gfx950 global_load_lds_dwordx4) -----------
+// Byte address of an LDS location (the value M0 takes for an LDS DMA).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+// Each lane fetches 16 bytes from gbase + voff and the hardware writes them
+// to LDS at m0 + 16 * lane: one instruction fills 1 KiB (16 rows of 64
+// bytes).  Written in assembly so that the compiler, which does not know
+// which LDS bytes a DMA writes, does not wait for every DMA in flight before
+// each LDS read; the pipeline's own waits (dma_wait_barrier) order them.
+__device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t m0) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(gbase), "{m0}"(m0)
+               : "memory");
+}
+// Wait until at most N of this wave's vector memory operations are in
+// flight (the oldest complete first), then a workgroup barrier: every wave's
+// DMAs issued before its last N have landed in LDS, and every wave has
+// finished the LDS reads it issued before the barrier.
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// acc += A x B^T over one 32-deep step, as mma_64x128, with the fragment LDS
+// reads in assembly: used where the LDS holds direct-load stages, so that
+// the compiler (which cannot tell them apart from the DMAs in flight) does
+// not make them wait for those.  The reads are issued in the order the
+// MFMAs consume them (a0 b0..b3, a1..a3, b4..b7) and waited for with
+// lgkmcnt counts (LDS reads complete in order) tied to the fragment
+// registers, so no MFMA can be scheduled before its wait.
+__device__ __forceinline__ void mma_64x128_dsasm(const bf16_t* A, const bf16_t* B, int lane, int arow,
+                                                 int brow, floatx4 (&acc)[4][8]) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  const uint32_t a = lds_addr(A) + (uint32_t)(2 * lds_off(arow + (lane & 15), lane >> 4));
+  const uint32_t b = lds_addr(B) + (uint32_t)(2 * lds_off(brow + (lane & 15), lane >> 4));
+  u32x4_t af[4], bf[8];
+#define BDH_DSR(dst, addr, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "n"(off))
+  BDH_DSR(af[0], a, 0);
+  BDH_DSR(bf[0], b, 0);
+  BDH_DSR(bf[1], b, 1024);
+  BDH_DSR(bf[2], b, 2048);
+  BDH_DSR(bf[3], b, 3072);
+  BDH_DSR(af[1], a, 1024);
+  BDH_DSR(af[2], a, 2048);
+  BDH_DSR(af[3], a, 3072);
+  BDH_DSR(bf[4], b, 4096);
+  BDH_DSR(bf[5], b, 5120);
+  BDH_DSR(bf[6], b, 6144);
+  BDH_DSR(bf[7], b, 7168);
+#undef BDH_DSR
+  auto mm = [&](int mi, int ni) {
+    acc[mi][ni] = mfma16(__builtin_bit_cast(bf16x8, af[mi]), __builtin_bit_cast(bf16x8, bf[ni]), acc[mi][ni]);
+  };
+  asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(af[0]), "+v"(bf[0]), "+v"(bf[1]), "+v"(bf[2]), "+v"(bf[3]));
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) mm(0, ni);
+  asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(af[1]), "+v"(af[2]), "+v"(af[3]));
+#pragma unroll
+  for (int mi = 1; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) mm(mi, ni);
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bf[4]), "+v"(bf[5]), "+v"(bf[6]), "+v"(bf[7]));
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 4; ni < 8; ++ni) mm(mi, ni);
+}
+
+// Register-set index of a two-set stage, as a compile-time constant.
+template <int S>
+using Set = std::integral_constant<int, S>;
+
+// As run_steps, for operands rotated by RoPE from a (cos, sin) table: the
+// table words of a 16-byte x chunk are only fetched when the chunk is
+// nonzero (ReLU activations leave most chunks zero), so x must be in
+// registers before its table loads are issued.  x of step kt is loaded two
+// steps ahead into register set (kt - kb) & 1, the table (and any other
+// operand) one step ahead, masked by that x; store(buf, set) rotates set's
+// step and writes it to LDS buffer buf.  Steps [kb, ke), an even count >= 2.
+template <class LoadX, class LoadT, class Store, class Compute>
+__device__ __forceinline__ void run_steps_x2(int kb, int ke, LoadX&& loadx, LoadT&& loadt,
+                                             Store&& store, Compute&& compute) {
+  loadx(kb, Set<0>{});
+  loadx(kb + 1, Set<1>{});
+  loadt(kb, Set<0>{});
+  store(0, Set<0>{});
+  __syncthreads();
+  for (int kt = kb; kt < ke; kt += 2) {
+    loadt(kt + 1, Set<1>{});
+    if (kt + 2 < ke) loadx(kt + 2, Set<0>{});
+    compute(0);
+    store(1, Set<1>{});
+    __syncthreads();
+    if (kt + 2 < ke) {
+      loadt(kt + 2, Set<0>{});
+      if (kt + 3 < ke) loadx(kt + 3, Set<1>{});
+    }
+    compute(1);
+    if (kt + 2 < ke) store(0, Set<0>{});
+    __syncthreads();
+  }
+}
+
+// True when any of the 8 bf16 of a chunk is nonzero (the sign bit ignored).
+__device__ __forceinline__ bool chunk_nonzero(uint4 x) {
+  return ((x.x | x.y | x.z | x.w) & 0x7fff7fffu) != 0;
+}
+
+// 16-byte table load for a nonzero x chunk; zeros otherwise (the rotation of
+// a zero chunk is zero whatever the table holds).
+__device__ __forceinline__ uint4 ldg16_if(bool on, const void* base, uint32_t byte_off) {
+  uint4 t = make_uint4(0, 0, 0, 0);
+  if (on) t = ldg16_off(base, byte_off);
+  return t;
 }
 
 }  // namespace mfma

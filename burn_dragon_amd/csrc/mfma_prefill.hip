@@ -38,7 +38,9 @@ using namespace mfma;
 // N range [kb, ke) in BK steps.  PAIR: two diagonal 128 x 128 blocks, rows
 // and columns ri .. ri+127 (waves 0, 1) and rj .. rj+127 (waves 2, 3; rj < 0:
 // none), each the lower part of a 256-row block's last 128-column tile.
-template <bool ROPE, bool DECAY, bool WHOLE, bool PAIR = false>
+// INNER: the 128 columns are tokens of the tile's own 256 rows (rj - ri = 0
+// or 128; pairs are inner too), so only the 4 A groups are loaded.
+template <bool ROPE, bool DECAY, bool WHOLE, bool INNER, bool PAIR = false>
 __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int64_t s, int kp,
                                           int64_t iv, int64_t ri, int64_t rj) {
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
@@ -60,39 +62,53 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   // 128) takes its B operand from the A rows already in LDS: groups 4 and 5
   // load nothing.  The row offset is a multiple of 8, so a row's swizzle is
   // the same seen from either base.
-  const bool inner = PAIR || (rj >= ri && rj + T256 / 2 <= ri + T256);
-  const int groups = inner ? 4 : 6;
+  constexpr bool inner = PAIR || INNER;
+  constexpr int groups = inner ? 4 : 6;
   const int64_t rj2 = PAIR ? (rj < 0 ? ri : rj) : rj;  // second block (a pair's absent one re-reads the first)
   const int kc = tid & 3, rb = tid >> 2;
   const uint32_t lane_off = (uint32_t)(rb * rowb + kc * 16);
-  struct Stage {
-    uint4 xr[6], cr[6];
-  } st;
-  auto load = [&](int kt) {
+  // Uniform base and per-lane offset of group g's 16 bytes of step kt in a
+  // [token][N] array (x, or the table, whose rows have the same byte pitch).
+  auto at = [&](int g, int kt, uint32_t& off) -> int64_t {
     const int64_t kofs = (int64_t)kt * 64;  // 32 bf16 of x, 16 words of the table
+    const int64_t r0 = PAIR ? (g < 2 ? ri + 64 * g : rj2 + 64 * (g - 2))
+                            : (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
+    if (WHOLE) {
+      off = lane_off;
+      return r0 * rowb + kofs;
+    }
+    const int64_t t = r0 + rb;
+    off = (uint32_t)((t < Lc ? t : Lc - 1) * rowb + kc * 16);
+    return kofs;
+  };
+  struct Stage {
+    uint4 xr[2][6], cr[6];
+  } st;
+  auto loadx = [&](int kt, auto set) {
 #pragma unroll
     for (int g = 0; g < 6; ++g) {
       if (g >= groups) break;
-      const int64_t r0 = PAIR ? (g < 2 ? ri + 64 * g : rj2 + 64 * (g - 2))
-                              : (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
-      if (WHOLE) {
-        const int64_t o = r0 * rowb + kofs;
-        st.xr[g] = ldg16_off(X + o, lane_off);
-        if (ROPE) st.cr[g] = ldg16_off(CS + o, lane_off);
-      } else {
-        const int64_t t = r0 + rb;
-        const uint32_t o = (uint32_t)((t < Lc ? t : Lc - 1) * rowb + kc * 16);
-        st.xr[g] = ldg16_off(X + kofs, o);
-        if (ROPE) st.cr[g] = ldg16_off(CS + kofs, o);
-      }
+      uint32_t off;
+      const int64_t o = at(g, kt, off);
+      st.xr[decltype(set)::value][g] = ldg16_off(X + o, off);
     }
   };
-  auto store = [&](int buf) {
+  auto loadt = [&](int kt, auto set) {
+#pragma unroll
+    for (int g = 0; g < 6; ++g) {
+      if (g >= groups) break;
+      uint32_t off;
+      const int64_t o = at(g, kt, off);
+      st.cr[g] = ldg16_if(chunk_nonzero(st.xr[decltype(set)::value][g]), CS + o, off);
+    }
+  };
+  auto store = [&](int buf, auto set) {
     bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
 #pragma unroll
     for (int g = 0; g < 6; ++g) {
       if (g >= groups) break;
-      *reinterpret_cast<uint4*>(&base[lds_off(64 * g + rb, kc)]) = prep8<ROPE>(st.xr[g], st.cr[g], 1.0f, false);
+      *reinterpret_cast<uint4*>(&base[lds_off(64 * g + rb, kc)]) =
+          prep8<ROPE>(st.xr[decltype(set)::value][g], st.cr[g], 1.0f, false);
     }
   };
 
@@ -105,9 +121,80 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   const int64_t wr0 = PAIR ? wc0 + 64 * (w & 1) : ri + 64 * w;
   const bool active = PAIR ? (wr0 < Lc && (w < 2 || rj >= 0)) : (wr0 + 64 > rj + 1 && wr0 < Lc);
   const int brow = PAIR ? 128 * (w >> 1) : inner ? (int)(rj - ri) : T256;  // LDS row of the first B row
-  run_steps(kb, ke, load, store, [&](int buf) {
+  auto compute = [&](int buf) {
     if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF, lane, 64 * w, brow, acc);
-  });
+  };
+  if (!ROPE) {
+    // Operands need no rotation: a three-stage LDS ring filled by direct
+    // loads two steps ahead, one barrier per step, no register staging.
+    // Stage rows are those of the register path (A rows 0..255, B rows
+    // 256..383), swizzled the same way: the lane writing LDS slot c of row r
+    // fetches global chunk c ^ ((r >> 1) & 3).  Wave w issues the DMAs of
+    // 16-row blocks w, w + 4, ... (groups of them per step).
+    const uint32_t gc = (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
+    uint32_t voff[groups];
+    int64_t vbase[groups];
+#pragma unroll
+    for (int j = 0; j < groups; ++j) {
+      const int blk = w + 4 * j;  // 16-row block of the stage
+      const int g = blk >> 2;
+      const int64_t r0 = PAIR ? (g < 2 ? ri + 64 * g : rj2 + 64 * (g - 2))
+                              : (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
+      const int64_t t = r0 + 16 * (blk & 3) + (lane >> 2);
+      if (WHOLE) {
+        vbase[j] = (r0 + 16 * (blk & 3)) * rowb;
+        voff[j] = (uint32_t)((lane >> 2) * rowb) + gc * 16;
+      } else {
+        vbase[j] = 0;
+        voff[j] = (uint32_t)((t < Lc ? t : Lc - 1) * rowb) + gc * 16;
+      }
+    }
+    constexpr int STAGE = groups * 64 * BK;  // bf16 elements of one stage
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+    auto issue = [&](int kt, int stg) {
+      const char* gb = X + (int64_t)kt * 64;
+#pragma unroll
+      for (int j = 0; j < groups; ++j)
+        dma16(gb + vbase[j], voff[j], lds0 + (uint32_t)(stg * STAGE * 2 + (w + 4 * j) * 1024));
+    };
+    // A compiler-visible wait: loads of other unit kinds that share this
+    // kernel's registers are then known complete, so the compiler adds no
+    // waits inside the ring loop (it cannot see the DMAs, only their
+    // destination-less assembly).
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    issue(kb, 0);
+    issue(kb + 1 < ke ? kb + 1 : kb, 1);
+    int stg = 0;
+    for (int kt = kb; kt < ke; ++kt) {
+      dma_wait_barrier<groups>();
+      // Step kt + 2 goes to the stage read in step kt - 1, which every wave
+      // has finished; past the end the last step is fetched again (unused),
+      // so that every step leaves the same number of DMAs in flight.
+      issue(kt + 2 < ke ? kt + 2 : ke - 1, stg == 0 ? 2 : stg - 1);
+      if (active) mma_64x128_dsasm(lds + stg * STAGE, lds + stg * STAGE, lane, 64 * w, brow, acc);
+      stg = stg == 2 ? 0 : stg + 1;
+    }
+    dma_wait_barrier<0>();  // the epilogue reuses the ring
+  } else if (ROPE && inner) {
+    // Two x sets of 4 chunks fit the register budget beside the
+    // accumulators; outer tiles (6 chunks) load x and the whole table one
+    // step ahead.
+    run_steps_x2(kb, ke, loadx, loadt, store, compute);
+  } else {
+    run_steps(kb, ke,
+              [&](int kt) {
+                loadx(kt, Set<0>{});
+                if (ROPE) {
+#pragma unroll
+                  for (int g = 0; g < groups; ++g) {
+                    uint32_t off;
+                    const int64_t o = at(g, kt, off);
+                    st.cr[g] = ldg16_off(CS + o, off);
+                  }
+                }
+              },
+              [&](int buf) { store(buf, Set<0>{}); }, compute);
+  }
 
   // Scores of rows ti < Lc and columns tj < Lc: times d^(ti - tj) below
   // the diagonal, 0 on and above it.  Waves that computed nothing still
@@ -162,41 +249,58 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
   const int kc = tid & 3, vb = tid >> 2;
   const int64_t vrow = a.Tp * 2;
   const uint32_t vlane = (uint32_t)(vb * vrow + kc * 16);
-  struct Stage {
-    uint4 xr[2], cr[2], vr[4];
-  } st;
-  int cur = 0;
-  auto load = [&](int kt) {
-    cur = kt;
+  // Uniform base and per-lane offset of token tb + i's 16 bytes for this
+  // lane in a [token][N] array (x, or the table: same byte pitch).
+  auto at = [&](int kt, int i, uint32_t& off) -> int64_t {
     const int64_t tb = t0 + (int64_t)kt * BK;
+    if (WHOLE) {
+      off = xlane;
+      return (tb + i) * rowb;
+    }
+    const int64_t t = tb + 2 * tp + i;
+    off = (uint32_t)((t < a.T ? t : a.T - 1) * rowb + (n0 + 8 * nv) * 2);
+    return 0;
+  };
+  struct Stage {
+    uint4 xr[2][2], cr[2], vr[4];
+  } st;
+  int cur[2] = {0, 0};  // step held by each x set
+  auto loadx = [&](int kt, auto set) {
+    cur[decltype(set)::value] = kt;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      if (WHOLE) {
-        const int64_t o = (tb + i) * rowb;
-        st.xr[i] = ldg16_off(X + o, xlane);
-        if (ROPE) st.cr[i] = ldg16_off(CS + o, xlane);
-      } else {
-        const int64_t t = tb + 2 * tp + i;
-        const uint32_t o = (uint32_t)((t < a.T ? t : a.T - 1) * rowb + (n0 + 8 * nv) * 2);
-        st.xr[i] = ldg16_off(X, o);
-        if (ROPE) st.cr[i] = ldg16_off(CS, o);
-      }
+      uint32_t off;
+      const int64_t o = at(kt, i, off);
+      st.xr[decltype(set)::value][i] = ldg16_off(X + o, off);
     }
+  };
+  auto loadv = [&](int kt) {
+    const int64_t tb = t0 + (int64_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < 4; ++i) st.vr[i] = ldg16_off(VT + (d0 + 64 * i) * vrow + tb * 2, vlane);
   };
-  auto store = [&](int buf) {
+  auto loadt = [&](int kt, auto set) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t off;
+      const int64_t o = at(kt, i, off);
+      st.cr[i] = ldg16_if(chunk_nonzero(st.xr[decltype(set)::value][i]), CS + o, off);
+    }
+    loadv(kt);
+  };
+  auto store = [&](int buf, auto set) {
+    constexpr int S = decltype(set)::value;
     bf16_t* A = lds + buf * BUF;             // [n][t], 128 rows
     bf16_t* B = lds + buf * BUF + 128 * BK;  // [d][t], 256 rows
     float f0[8], f1[8];
     float w0 = 1.0f, w1 = 1.0f;
     if (DECAY) {
-      const int64_t tl = (int64_t)cur * BK + 2 * tp;
+      const int64_t tl = (int64_t)cur[S] * BK + 2 * tp;
       w0 = tl < Lc ? decay_pow_int(dk, l2d, (int)(Lc - tl)) : 0.0f;
       w1 = tl + 1 < Lc ? decay_pow_int(dk, l2d, (int)(Lc - tl - 1)) : 0.0f;
     }
-    prep8_f32<ROPE>(st.xr[0], st.cr[0], w0, DECAY, f0);
-    prep8_f32<ROPE>(st.xr[1], st.cr[1], w1, DECAY, f1);
+    prep8_f32<ROPE>(st.xr[S][0], st.cr[0], w0, DECAY, f0);
+    prep8_f32<ROPE>(st.xr[S][1], st.cr[1], w1, DECAY, f1);
     uint32_t* Aw = reinterpret_cast<uint32_t*>(A);
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -209,9 +313,15 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
   zero_acc(acc);
   const bool active = d0 + wn * 128 < a.D;
   const int nk = (int)(((Lc + 63) / 64) * 2);  // even; steps past Lc read zero v columns
-  run_steps(0, nk, load, store, [&](int buf) {
+  auto compute = [&](int buf) {
     if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + 128 * BK, lane, 64 * wm, 128 * wn, acc);
-  });
+  };
+  if (ROPE) {
+    run_steps_x2(0, nk, loadx, loadt, store, compute);
+  } else {
+    run_steps(0, nk, [&](int kt) { loadx(kt, Set<0>{}); loadv(kt); }, [&](int buf) { store(buf, Set<0>{}); },
+              compute);
+  }
 
   // Columns past D (zero v^T rows) are computed and never written; D is a
   // multiple of 32, so a float4 of columns is all in or all out.
@@ -384,7 +494,8 @@ __device__ __forceinline__ void tile_of(int u, int& rbk, int& cbk) {
 
 template <bool ROPE, bool DECAY>
 __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * BUF];
+  // Two register-path buffers, or the three-stage ring of the direct-load gram.
+  __shared__ __attribute__((aligned(16))) bf16_t lds[3 * BUF];
   const int id = blockIdx.x;
   // The table was complete before this launch began; name it for the next
   // call's prep kernel.
@@ -414,17 +525,23 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
       if (ra >= Lc) return;  // past a ragged last interval: never read
       if (2 * j + 1 >= a.nb || rb >= Lc) rb = -1;
       if (ra + T256 / 2 <= Lc && (rb < 0 || rb + T256 / 2 <= Lc))
-        gram_unit<ROPE, DECAY, true, true>(a, lds, s, kp, iv, ra, rb);
+        gram_unit<ROPE, DECAY, true, true, true>(a, lds, s, kp, iv, ra, rb);
       else
-        gram_unit<ROPE, DECAY, false, true>(a, lds, s, kp, iv, ra, rb);
+        gram_unit<ROPE, DECAY, false, true, true>(a, lds, s, kp, iv, ra, rb);
       return;
     }
     int rbk, cbk;
     tile_of(u, rbk, cbk);
     const int64_t ri = (int64_t)rbk * T256, rj = (int64_t)cbk * (T256 / 2);
     if (ri >= Lc || rj >= Lc) return;  // tile past a ragged last interval: never read
-    if (ri + T256 <= Lc) gram_unit<ROPE, DECAY, true>(a, lds, s, kp, iv, ri, rj);
-    else gram_unit<ROPE, DECAY, false>(a, lds, s, kp, iv, ri, rj);
+    const bool inner = rj >= ri && rj + T256 / 2 <= ri + T256;
+    if (ri + T256 <= Lc) {
+      if (inner) gram_unit<ROPE, DECAY, true, true>(a, lds, s, kp, iv, ri, rj);
+      else gram_unit<ROPE, DECAY, true, false>(a, lds, s, kp, iv, ri, rj);
+    } else {
+      if (inner) gram_unit<ROPE, DECAY, false, true>(a, lds, s, kp, iv, ri, rj);
+      else gram_unit<ROPE, DECAY, false, false>(a, lds, s, kp, iv, ri, rj);
+    }
   } else if (id < a.gram_ids + a.rd_units) {
     // readout unit: (stream, 256-row block, 128-column block, N range), N range fastest
     int rid = id - a.gram_ids;
