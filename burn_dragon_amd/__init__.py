@@ -17,6 +17,9 @@ from .attention import (CompiledDenseCausalAttentionPlan,  # noqa: F401
                         try_fused_dense_causal_attention,
                         try_fused_dense_causal_attention_wgpu,
                         try_fused_dense_causal_attention_with_plan)
+from .backward import (DenseCausalAttentionVjp, RecurrentAttentionGrads,  # noqa: F401
+                       dense_causal_attention_vjp, dense_causal_attention_vjp_with_initial_rho,
+                       recurrent_attention_vjp)
 from .decode import DecodeOutput, decode_step  # noqa: F401
 from .layer import LowRankLayerOutput, LowRankWeights, lowrank_layer_forward  # noqa: F401
 from .model import (BdhModelState, BdhModelWeights, model_forward_logits, new_model_state,  # noqa: F401

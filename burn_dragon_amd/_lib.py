@@ -66,6 +66,8 @@ SIGNATURES = {
                                                     _vp, _vp, _vp, _vp]),
     "bdh_dense_causal_attention_fwd": (_i32, [ctypes.POINTER(BdhRecurrentPlan), _i32, _vp, _vp,
                                               _vp, _vp, _vp]),
+    "bdh_dense_causal_attention_vjp": (_i32, [ctypes.POINTER(BdhRecurrentPlan)] + [_vp] * 10),
+    "bdh_recurrent_attention_vjp": (_i32, [ctypes.POINTER(BdhRecurrentPlan)] + [_vp] * 10),
     "bdh_lowrank_pack_weights": (_i32, [_i64] * 3 + [_vp] * 7),
     "bdh_lowrank_layer_fwd": (_i32, [ctypes.POINTER(BdhLayerPlan), _vp, _vp, _vp, _vp,
                                      ctypes.POINTER(BdhRope), _vp, _vp, _vp, _vp]),

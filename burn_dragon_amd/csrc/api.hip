@@ -502,6 +502,62 @@ bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads, in
 
 bdh_status bdh_scratch_release(void* stream) { return scratch_release((hipStream_t)stream); }
 
+static bdh_status vjp_common(const bdh_recurrent_plan* plan, const float* query, const float* value,
+                             const float* decay, const float* rho0, const float* grad_out,
+                             float* grad_query, float* grad_value, float* grad_decay, float* grad_rho0,
+                             void* stream, bool recurrent) {
+  ProfScope prof;
+  bdh_status st = check_plan(plan);
+  if (st != BDH_OK) return st;
+  if (!query || !value || !grad_out || !grad_query || !grad_value)
+    return fail(BDH_EINVAL, "null tensor pointer");
+  if (grad_rho0 && !rho0) return fail(BDH_EINVAL, "grad_rho0 needs the initial state rho0");
+  for (const void* t : {(const void*)query, (const void*)value, (const void*)decay, (const void*)rho0,
+                        (const void*)grad_out, (const void*)grad_query, (const void*)grad_value,
+                        (const void*)grad_decay, (const void*)grad_rho0})
+    if (((uintptr_t)t & 3) != 0) return fail(BDH_EINVAL, "tensor pointers must be 4-byte aligned");
+  if (plan->time > 4096) return fail(BDH_UNSUPPORTED, "the attention VJP needs time <= 4096");
+  if (plan->latent > ((int64_t)1 << 24) || plan->embd > ((int64_t)1 << 24))
+    return fail(BDH_UNSUPPORTED, "latent and embd must be below 2^24");
+  VjpArgs a;
+  a.q = query;
+  a.v = value;
+  a.decay = decay;
+  a.rho0 = rho0;
+  a.g = grad_out;
+  a.grad_q = grad_query;
+  a.grad_v = grad_value;
+  a.grad_decay = grad_decay;
+  a.grad_rho0 = grad_rho0;
+  a.B = plan->batch;
+  a.H = plan->heads;
+  a.Hv = plan->value_heads;
+  a.T = plan->time;
+  a.N = plan->latent;
+  a.D = plan->embd;
+  a.recurrent_eps = recurrent;
+  st = run_attention_vjp(a, (hipStream_t)stream, &prof.launches);
+  if (st != BDH_OK) return st;
+  prof.done(true);
+  return BDH_OK;
+}
+
+bdh_status bdh_dense_causal_attention_vjp(const bdh_recurrent_plan* plan, const float* query,
+                                          const float* value, const float* decay, const float* rho0,
+                                          const float* grad_output, float* grad_query, float* grad_value,
+                                          float* grad_decay, float* grad_rho0, void* stream) {
+  return vjp_common(plan, query, value, decay, rho0, grad_output, grad_query, grad_value, grad_decay,
+                    grad_rho0, stream, false);
+}
+
+bdh_status bdh_recurrent_attention_vjp(const bdh_recurrent_plan* plan, const float* query,
+                                       const float* value, const float* rho_in, const float* decay,
+                                       const float* grad_context, float* grad_query, float* grad_value,
+                                       float* grad_rho, float* grad_decay, void* stream) {
+  return vjp_common(plan, query, value, decay, rho_in, grad_context, grad_query, grad_value, grad_decay,
+                    grad_rho, stream, true);
+}
+
 bdh_status bdh_lowrank_pack_weights(int64_t heads, int64_t latent, int64_t embd,
                                     const float* encoder, const float* encoder_v,
                                     const float* decoder, void* encoder_packed,

@@ -41,6 +41,11 @@ enum ScratchSlot {
   SLOT_DECODE_PART,  // decode range readouts        [S, G, D] f32
   SLOT_DECODE_IDX,   // decode range active lists    [S, N] int32
   SLOT_DECODE_CNT,   // decode range active counts   [S, G] int32
+  SLOT_VJP_S,        // VJP scores tril(QQ^T) * D    [S, T, T] f32
+  SLOT_VJP_GS,       // VJP tril(G V^T)              [S, T, T] f32
+  SLOT_VJP_M,        // VJP GS*D + its transpose     [S, T, T] f32
+  SLOT_VJP_TD,       // VJP per-head grad_v, IC, G*d^t  3 x [S, T, D] f32
+  SLOT_VJP_PART,     // VJP decay partials           [S] f64
   SLOT_COUNT
 };
 // Scratch of the calling stream (see api.hip): grows on first use of a
@@ -153,6 +158,22 @@ struct DecodeArgs {
   size_t part_bytes = 0;
 };
 bdh_status run_decode(const DecodeArgs& a, hipStream_t st, uint64_t* launches);
+
+// --- attention VJP (vjp.hip), fp32 ---------------------------------------------
+struct VjpArgs {
+  const float* q;       // [S, T, N] (Q = K)
+  const float* v;       // [B, Hv, T, D]
+  const float* decay;   // [H] or null (ones)
+  const float* rho0;    // [S, N, D] or null
+  const float* g;       // context gradient [S, T, D]
+  float* grad_q;        // [S, T, N]
+  float* grad_v;        // [B, Hv, T, D]
+  float* grad_decay;    // [H] or null (not computed)
+  float* grad_rho0;     // [S, N, D] or null (not computed)
+  int64_t B, H, Hv, T, N, D;
+  bool recurrent_eps;   // decay guard of the recurrent backward, else d + 1e-12
+};
+bdh_status run_attention_vjp(const VjpArgs& a, hipStream_t st, uint64_t* launches);
 // Bytes of range buffers run_decode needs for a.
 size_t decode_part_bytes(const DecodeArgs& a);
 

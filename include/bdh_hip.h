@@ -159,6 +159,37 @@ bdh_status bdh_dense_causal_attention_fwd(const bdh_recurrent_plan* plan, int32_
                                           const float* decay, float* context_out,
                                           void* stream);
 
+/* VJP of the dense causal attention, fp32 (the reference's backward runs in
+ * f32).  Replaces dense_causal_attention_vjp and
+ * dense_causal_attention_vjp_with_initial_rho
+ * (crates/burn_dragon_kernel/src/dense_causal_attention/backward_runtime.rs
+ * :16-148): for ctx = tril(-1)(Q Q^T * d^(r-c)) V + (Q * d^t) rho0 and the
+ * context gradient G [B,H,T,D]:
+ *   grad_query [B,H,T,N], grad_value [B,Hv,T,D] (summed over heads when
+ *   Hv = 1), grad_decay [H] (sum((G V^T * gap) * S) / (d + 1e-12) and the
+ *   state term), grad_rho0 [B,H,N,D] = (Q * d^t)^T G.
+ * decay NULL = ones; rho0 NULL = no state (grad_rho0 must then be NULL);
+ * grad_decay and grad_rho0 may be NULL (not computed).  time <= 4096
+ * (BDH_UNSUPPORTED beyond); pointers 4-byte aligned. */
+bdh_status bdh_dense_causal_attention_vjp(const bdh_recurrent_plan* plan, const float* query,
+                                          const float* value, const float* decay, const float* rho0,
+                                          const float* grad_output, float* grad_query,
+                                          float* grad_value, float* grad_decay, float* grad_rho0,
+                                          void* stream);
+
+/* Backward of the recurrent attention with respect to its context output
+ * (FusedRecurrentAttentionBackward, crates/burn_dragon_kernel/src/recurrent/
+ * backward_runtime.rs:336-502, 1155-1239: grad query / value / decay from the
+ * state history and the reverse-time adjoint, and the initial state's
+ * gradient).  The same closed form as bdh_dense_causal_attention_vjp, with the
+ * recurrent kernel's decay guard (|d| < 1e-8 -> 1e-8, :458-465).
+ * rho_in NULL = zeros (grad_rho must then be NULL); decay NULL = ones. */
+bdh_status bdh_recurrent_attention_vjp(const bdh_recurrent_plan* plan, const float* query,
+                                       const float* value, const float* rho_in, const float* decay,
+                                       const float* grad_context, float* grad_query,
+                                       float* grad_value, float* grad_rho, float* grad_decay,
+                                       void* stream);
+
 /* Low-rank BDH layer body around the recurrent attention, bf16 MFMA with
  * fp32 accumulation.  Replaces lowrank_residual_step_impl
  * (crates/burn_dragon_core/src/model/residual_stream.rs:323-572) with its

@@ -263,3 +263,57 @@ def rel_l2(a, b) -> float:
     den = np.linalg.norm(b.ravel())
     num = np.linalg.norm((a - b).ravel())
     return float(num / den) if den > 0 else float(num)
+
+
+def attention_vjp_f64(q, v, grad_out, decay=None, rho0=None, safe: str = "dense"):
+    """VJP of the causal linear attention (the context only) in f64:
+    ctx = tril(-1)(Q Q^T * d^(r-c)) V + (Q * d^t) rho0, Q = K = query.
+    Restates dense_causal_attention_vjp_with_initial_rho
+    (kernel/src/dense_causal_attention/backward_runtime.rs:36-148), which the
+    recurrent backward (kernel/src/recurrent/backward_runtime.rs:336-502,
+    state history + reverse-time adjoint) equals in closed form:
+      S  = tril(-1)(Q Q^T) * D,  D[r, c] = d^(r-c)          (:70-72)
+      GS = tril(-1)(G V^T)                                   (:90-93)
+      grad_v = S^T G  (summed over heads when value heads = 1)  (:80-89)
+      grad_q = (GS*D + (GS*D)^T) Q  [+ (G rho0^T) * d^t]     (:94-98, :124-125)
+      grad_d = sum(GS * gap * S) / sd  [+ sum(G * (Q d^t rho0) * t) / sd]
+      grad_rho0 = (Q * d^t)^T G                               (:137)
+    sd = d + 1e-12 (safe="dense", :100) or, for |d| < 1e-8, 1e-8
+    (safe="recurrent", recurrent/backward_runtime.rs:458-465).
+    q [B,H,T,N], v [B,Hv,T,D], grad_out [B,H,T,D], decay [H] (None = ones),
+    rho0 [B,H,N,D] or None.  Returns (grad_q, grad_v, grad_decay, grad_rho0)."""
+    q = np.asarray(q, np.float64)
+    v = np.asarray(v, np.float64)
+    g = np.asarray(grad_out, np.float64)
+    B, H, T, N = q.shape
+    Hv, D = v.shape[1], v.shape[3]
+    d = np.ones(H) if decay is None else np.asarray(decay, np.float64)
+    if safe == "dense":
+        sd = d + 1e-12
+    else:
+        sd = np.where((d < 1e-8) & (d > -1e-8), 1e-8, d)
+    vh = np.broadcast_to(v, (B, H, T, D)) if Hv == 1 else v
+    r = np.arange(T)[:, None]
+    c = np.arange(T)[None, :]
+    gap = np.where(r > c, r - c, 0).astype(np.float64)
+    below = r > c
+    Dm = np.power(d[:, None, None], gap[None])              # [H, T, T]
+    S = np.where(below, q @ q.transpose(0, 1, 3, 2), 0.0) * Dm[None]
+    GS = np.where(below, g @ vh.transpose(0, 1, 3, 2), 0.0)
+    W = GS * Dm[None]
+    gq = (W + W.transpose(0, 1, 3, 2)) @ q
+    gv = S.transpose(0, 1, 3, 2) @ g
+    if Hv == 1:
+        gv = gv.sum(axis=1, keepdims=True)
+    gd = ((GS * gap[None, None]) * S / sd[None, :, None, None]).sum(axis=(0, 2, 3))
+    grho = None
+    if rho0 is not None:
+        rho = np.asarray(rho0, np.float64)
+        pos = np.arange(T, dtype=np.float64)
+        sdec = np.power(d[:, None], pos[None])[None, :, :, None]   # [1, H, T, 1]
+        sq = q * sdec
+        ic = sq @ rho
+        gq = gq + (g @ rho.transpose(0, 1, 3, 2)) * sdec
+        gd = gd + ((g * ic) * pos[None, None, :, None] / sd[None, :, None, None]).sum(axis=(0, 2, 3))
+        grho = sq.transpose(0, 1, 3, 2) @ g
+    return gq, gv, gd, grho
