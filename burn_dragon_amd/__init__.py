@@ -22,5 +22,5 @@ from .backward import (DenseCausalAttentionVjp, RecurrentAttentionGrads,  # noqa
                        recurrent_attention_vjp)
 from .decode import DecodeOutput, decode_step  # noqa: F401
 from .layer import LowRankLayerOutput, LowRankWeights, lowrank_layer_forward  # noqa: F401
-from .model import (BdhModelState, BdhModelWeights, model_forward_logits, new_model_state,  # noqa: F401
-                    pack_model)
+from .model import (BdhModelState, BdhModelWeights, load_model_state, model_forward_logits,  # noqa: F401
+                    new_model_state, pack_model, save_model_state)

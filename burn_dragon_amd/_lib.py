@@ -40,6 +40,12 @@ class BdhLayerPlan(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in ("batch", "heads", "time", "latent", "embd")]
 
 
+class BdhLayerStateDesc(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int64), ("heads", ctypes.c_int64), ("latent", ctypes.c_int64),
+                ("embd", ctypes.c_int64), ("persist_sequence_state", ctypes.c_int32),
+                ("retain_terminal_sequence_state", ctypes.c_int32)]
+
+
 class BdhProfileSnapshot(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in (
         "calls", "launches", "total_ns", "setup_ns", "copy_ns", "dispatch_ns",
@@ -74,6 +80,12 @@ SIGNATURES = {
     "bdh_embed_norm": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
     "bdh_lm_head_pack": (_i32, [_i64, _i64, _vp, _vp, _vp]),
     "bdh_lm_logits": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "bdh_state_record_save": (_i32, [ctypes.c_char_p, _i64, _i32, ctypes.POINTER(BdhLayerStateDesc),
+                                     ctypes.POINTER(_vp), _vp]),
+    "bdh_state_record_info": (_i32, [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.POINTER(_i32),
+                                     ctypes.POINTER(BdhLayerStateDesc), _i32]),
+    "bdh_state_record_load": (_i32, [ctypes.c_char_p, _i32, ctypes.POINTER(BdhLayerStateDesc),
+                                     ctypes.POINTER(_vp), _vp]),
     "bdh_profile_enable": (None, [_i32]),
     "bdh_profile_reset": (None, []),
     "bdh_profile_get": (None, [ctypes.POINTER(BdhProfileSnapshot)]),

@@ -121,3 +121,61 @@ def model_forward_logits(tokens: torch.Tensor, weights: BdhModelWeights, *,
     if state is not None:
         state.position += T
     return logits
+
+
+def save_model_state(path: str, state: BdhModelState, persist_sequence_state: bool = True,
+                     retain_terminal_sequence_state: bool = True) -> None:
+    """Writes the state's position and every layer's rho (a layer whose rho is
+    None has no rho) to a state record (bdh_state_record_save; the
+    StreamingRuntimeStateRecord of runtime_checkpoint.rs:16-112 for this
+    path's state).  Raises on failure."""
+    n = len(state.rho)
+    descs = (_lib.BdhLayerStateDesc * max(n, 1))()
+    ptrs = (ctypes.c_void_p * max(n, 1))()
+    dev = None
+    for i, r in enumerate(state.rho):
+        if r is not None:
+            if r.dtype != torch.float32 or not r.is_cuda or r.dim() != 4 or not r.is_contiguous():
+                raise ValueError("rho must be a contiguous f32 [B,H,N,D] device tensor")
+            descs[i].batch, descs[i].heads, descs[i].latent, descs[i].embd = r.shape
+            ptrs[i] = r.data_ptr()
+            dev = r.device
+        descs[i].persist_sequence_state = int(persist_sequence_state)
+        descs[i].retain_terminal_sequence_state = int(retain_terminal_sequence_state)
+    stream = ctypes.c_void_p(_stream_ptr(dev)) if dev is not None else None
+    st = _lib.load().bdh_state_record_save(str(path).encode(), int(state.position), n, descs, ptrs,
+                                           stream)
+    if st != _lib.BDH_OK:
+        raise _lib.BdhError(f"bdh_state_record_save: {_lib.last_error()}")
+
+
+def load_model_state(path: str, device: torch.device) -> BdhModelState:
+    """Reads a state record into a new BdhModelState on `device` (rho None for
+    layers recorded without one).  Raises on a corrupt or unreadable record."""
+    lib = _lib.load()
+    pos, n = ctypes.c_int64(), ctypes.c_int32()
+    st = lib.bdh_state_record_info(str(path).encode(), ctypes.byref(pos), ctypes.byref(n), None, 0)
+    if st != _lib.BDH_OK:
+        raise _lib.BdhError(f"bdh_state_record_info: {_lib.last_error()}")
+    descs = (_lib.BdhLayerStateDesc * max(n.value, 1))()
+    st = lib.bdh_state_record_info(str(path).encode(), ctypes.byref(pos), ctypes.byref(n), descs,
+                                   n.value)
+    if st != _lib.BDH_OK:
+        raise _lib.BdhError(f"bdh_state_record_info: {_lib.last_error()}")
+    state = BdhModelState.__new__(BdhModelState)
+    state.position = int(pos.value)
+    state.rho = []
+    ptrs = (ctypes.c_void_p * max(n.value, 1))()
+    for i in range(n.value):
+        d = descs[i]
+        if d.batch == 0:
+            state.rho.append(None)
+            continue
+        r = torch.empty((d.batch, d.heads, d.latent, d.embd), device=device, dtype=torch.float32)
+        ptrs[i] = r.data_ptr()
+        state.rho.append(r)
+    st = lib.bdh_state_record_load(str(path).encode(), n.value, descs, ptrs,
+                                   ctypes.c_void_p(_stream_ptr(device)))
+    if st != _lib.BDH_OK:
+        raise _lib.BdhError(f"bdh_state_record_load: {_lib.last_error()}")
+    return state

@@ -250,6 +250,36 @@ bdh_status bdh_lm_logits(const float* hidden, int64_t rows, int64_t embd,
                          const void* lm_head_packed, int64_t vocab, float* logits,
                          void* stream);
 
+/* Streaming-state record: the model position and each layer's carried rho
+ * with its sequence-state flags, saved from / loaded into device memory.
+ * Replaces, for the state this path carries, StreamingRuntimeStateRecord /
+ * LayerRuntimeStateRecord (crates/burn_dragon_language/src/train/
+ * runtime_checkpoint.rs:16-112) over LayerState / ModelState
+ * (crates/burn_dragon_core/src/model/state.rs:7-30); Burn's bincode record
+ * cannot be written without Burn, so the file is this library's own
+ * little-endian layout (magic "BDHRHO01", version 1, n_layers, position,
+ * 64-byte layer entries, f32 rho blocks at 4096-byte offsets, a CRC32C per
+ * block).  A layer whose four dims are 0 has no rho (None).  Copies run on
+ * `stream` through pinned staging buffers (device-to-host overlapped with
+ * the file write); both calls return once the file / the device buffers are
+ * complete.  load rejects a record whose layer count or shapes differ from
+ * `layers` (BDH_EINVAL) and verifies every checksum after its copy (on a
+ * mismatch the layer's buffer holds the corrupt data and BDH_EINVAL is
+ * returned).  info reads the header only, so the caller can allocate. */
+typedef struct {
+  int64_t batch, heads, latent, embd;
+  int32_t persist_sequence_state, retain_terminal_sequence_state;
+} bdh_layer_state_desc;
+
+bdh_status bdh_state_record_save(const char* path, int64_t position, int32_t n_layers,
+                                 const bdh_layer_state_desc* layers, const float* const* rho,
+                                 void* stream);
+bdh_status bdh_state_record_info(const char* path, int64_t* position, int32_t* n_layers,
+                                 bdh_layer_state_desc* layers, int32_t max_layers);
+bdh_status bdh_state_record_load(const char* path, int32_t n_layers,
+                                 const bdh_layer_state_desc* layers, float* const* rho,
+                                 void* stream);
+
 /* Profiling counters with the field names of KernelProfileSnapshot
  * (crates/burn_dragon_kernel/src/profiling.rs:3-16), filled per entry-point
  * call as recurrent.rs:206-215, 344-356 fills them; collected only while
