@@ -93,6 +93,7 @@ SIGNATURES = {
     "bdh_profile_kernel_get": (_i32, [_i32, ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_int64)]),
     "bdh_scratch_release": (_i32, [_vp]),
+    "bdh_selftest_rot8": (_i32, [_vp] * 6 + [_i64, _vp]),
     "bdh_last_error": (ctypes.c_char_p, []),
     "bdh_version": (ctypes.c_char_p, []),
 }

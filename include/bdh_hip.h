@@ -325,6 +325,16 @@ bdh_status bdh_profile_kernel_get(int32_t kind, double* total_ms, int64_t* launc
  * after destroying every graph captured on it that calls this library. */
 bdh_status bdh_scratch_release(void* stream);
 
+/* Check hook, no counterpart in the reference: runs the hand-written RoPE
+ * rotation of the bf16 prefill (4 bf16 (even, odd) pairs per 16-byte chunk
+ * rotated by 4 packed bf16 (cos, sin) words) and the same rotation written
+ * with the compiler's dot-product builtin, on n_chunks chunks: rotated bf16
+ * chunks (RNE) and the 8 f32 results per chunk of each.  Used by the tests to
+ * hold the assembly block to the builtin bit for bit. */
+bdh_status bdh_selftest_rot8(const void* x, const void* cs, void* out_bf16_asm,
+                             void* out_bf16_builtin, float* out_f32_asm, float* out_f32_builtin,
+                             int64_t n_chunks, void* stream);
+
 /* Thread-local message of the last non-OK status of this thread. */
 const char* bdh_last_error(void);
 

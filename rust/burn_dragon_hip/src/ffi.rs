@@ -144,6 +144,9 @@ extern "C" {
     pub fn bdh_profile_kernel_timing(enabled: i32) -> i32;
     pub fn bdh_profile_kernel_get(kind: i32, total_ms: *mut f64, launches: *mut i64) -> i32;
     pub fn bdh_scratch_release(stream: *mut c_void) -> i32;
+    pub fn bdh_selftest_rot8(x: *const c_void, cs: *const c_void, out_bf16_asm: *mut c_void,
+                             out_bf16_builtin: *mut c_void, out_f32_asm: *mut f32,
+                             out_f32_builtin: *mut f32, n_chunks: i64, stream: *mut c_void) -> i32;
     pub fn bdh_last_error() -> *const c_char;
     pub fn bdh_version() -> *const c_char;
 }
