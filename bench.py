@@ -57,10 +57,12 @@ def parse():
     ap.add_argument("--model-decode-steps", type=int, default=32,
                     help="timed C5 greedy decode steps")
     ap.add_argument("--only", choices=("all", "prefill", "decode", "long", "model", "model-decode",
-                                       "copy"),
+                                       "f32", "copy", "rmw"),
                     default="all",
                     help="one leg only; 'copy' times a 1 GiB device copy (the calibration kernel "
-                         "of the FETCH_SIZE / WRITE_SIZE counter runs)")
+                         "of the FETCH_SIZE / WRITE_SIZE counter runs); 'rmw' measures the HBM "
+                         "ceilings (read, copy, in-place RMW, RMW of random 1 KiB rows) on a "
+                         "buffer the size of C3's rho")
     ap.add_argument("--long-steps", type=int, default=3, help="timed C4 prefills")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="target CPU-baseline wall time (split between prefill and decode)")
@@ -366,11 +368,55 @@ def cpu_baseline_prefill(target_s: float):
         O.ndarray_recurrent_f32(q, v, threads=threads)
         total += time.perf_counter() - t0
         passes += 1
+    # The same op sequence on one thread: one batch row (4 head streams) over
+    # an eighth of the tokens, so it takes about a quarter of the run above.
+    T1 = max(4, T // 8)
+    t0 = time.perf_counter()
+    q1 = O.rope_rotate(x[:1, :, :T1], pos0=0)
+    O.ndarray_recurrent_f32(q1, v[:1, :, :T1], threads=1)
+    secs1 = time.perf_counter() - t0
     return {"value": round(B * T * passes / total, 1), "unit": "tokens/s", "cores": threads,
-            "kind": "port", "host": _cpu_model(),
+            "kind": "port", "host": _cpu_model(), "nproc": _nproc(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
             "sample": f"C2 shapes (B8 nh4 N8192 D256), first {T} tokens x {passes} passes, fp32, "
                       f"RoPE + NdArray op-sequence recurrence (linear.rs:43-57) restated in C, "
-                      f"{total:.2f} s wall"}
+                      f"{total:.2f} s wall",
+            "one_thread": {"value": round(T1 / secs1, 2), "unit": "tokens/s", "cores": 1,
+                           "sample": f"C2 shapes, batch row 0 (4 head streams), first {T1} tokens, "
+                                     f"same op sequence, {secs1:.2f} s wall"},
+            "c1_full": cpu_c1_full(threads)}
+
+
+def _nproc() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def cpu_c1_full(threads: int):
+    """BASELINE config 1 timed in full on the CPU (B1 nh4 T256 N1024 D64, fp32,
+    V ~ N(0,1), RoPE theta 65536): the NdArray recurrent op sequence
+    (linear.rs:43-57) and the dense-score form (linear.rs:241, 321), each on
+    `threads` threads and on one (the four (b, h) streams bound the useful
+    thread count at 4)."""
+    import numpy as np
+    from oracle import oracle as O
+    B, H, T, N, D = 1, 4, 256, 1024, 64
+    rng = np.random.default_rng(SEED + 1)
+    x = np.maximum(rng.standard_normal((B, H, T, N), dtype=np.float32) - np.float32(1.645), 0)
+    v = rng.standard_normal((B, 1, T, D), dtype=np.float32)
+    out = {"shape": "B1 nh4 T256 N1024 D64, fp32"}
+    for th in (threads, 1):
+        t0 = time.perf_counter()
+        q = O.rope_rotate(x, pos0=0)
+        t_rope = time.perf_counter() - t0
+        _, _, t_rec = O.ndarray_recurrent_f32(q, v, threads=th)
+        _, t_dense = O.ndarray_dense_f32(q, v, threads=th)
+        out[f"threads_{th}"] = {"recurrent_form_ms": round((t_rope + t_rec) * 1e3, 2),
+                                "dense_score_form_ms": round((t_rope + t_dense) * 1e3, 2),
+                                "recurrent_tokens_per_s": round(B * T / (t_rope + t_rec), 1)}
+    return out
 
 
 def cpu_baseline_decode(target_s: float):
@@ -391,7 +437,7 @@ def cpu_baseline_decode(target_s: float):
         t_total += time.perf_counter() - t0
         steps += 1
     return {"value": round(B * steps / t_total, 1), "unit": "tokens/s", "cores": threads,
-            "kind": "port", "host": _cpu_model(),
+            "kind": "port", "host": _cpu_model(), "nproc": _nproc(),
             "sample": f"C3 shapes with B={B} (16 streams), {steps} steps, fp32, RoPE + NdArray "
                       f"op-sequence step over all N*D of rho, {t_total:.2f} s wall"}
 
@@ -516,6 +562,108 @@ def bench_copy(torch):
                       "read_plus_write_GBs": round(2 * 4 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
+def bench_f32(torch, args):
+    """The fp32 path, the one an unchanged f32 Burn model reaches (the
+    reference's fused op accepts F32 only, forward_runtime.rs:69-96), through
+    bdh_recurrent_attention_rope_fwd: BASELINE config 1 in full (B1 nh4 T256
+    N1024 D64, V ~ N(0,1)) and the C2 shape in fp32.  FLOP per call are the
+    recurrent form's 4*N*D per token and stream (the figure BASELINE quotes for
+    C1 as 0.268 GFLOP)."""
+    from burn_dragon_amd import _lib
+    lib = _lib.load()
+    dev = torch.device("cuda")
+    out = {}
+    for name, (B, H, T, N, D, vscale) in (("c1", (1, 4, 256, 1024, 64, 1.0)),
+                                          ("c2_shape", (8, 4, 512, 8192, 256, 1.0 / 16))):
+        g = torch.Generator(device=dev).manual_seed(SEED + 11)
+        x = torch.relu(torch.randn(B, H, T, N, generator=g, device=dev) - 1.645)
+        v = torch.randn(B, 1, T, D, generator=g, device=dev) * vscale
+        ctx = torch.empty(B, H, T, D, device=dev)
+        rho = torch.empty(B, H, N, D, device=dev)
+        plan = _lib.BdhRecurrentPlan(B, H, 1, T, N, D)
+        rope = _lib.BdhRope(_lib.BDH_ROPE_SEQUENTIAL, 0, 0, 65536.0)
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+        def call():
+            st = lib.bdh_recurrent_attention_rope_fwd(
+                ctypes.byref(plan), _lib.BDH_F32, ctypes.c_void_p(x.data_ptr()),
+                ctypes.c_void_p(v.data_ptr()), None, None, ctypes.byref(rope),
+                ctypes.c_void_p(ctx.data_ptr()), ctypes.c_void_p(rho.data_ptr()), 0, stream)
+            if st != 0:
+                raise RuntimeError(f"fp32 forward failed: {_lib.last_error()}")
+        for _ in range(3):
+            call()
+        steps = max(5, args.steps)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        flop = B * H * T * 4 * N * D
+        out[name] = {"shape": {"B": B, "nh": H, "T": T, "N": N, "D": D}, "ms_per_call": round(ms, 4),
+                     "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+                     "tflops_recurrent_form": round(flop / (ms * 1e-3) / 1e12, 2)}
+        print(f"[f32] {name}: {ms:.3f} ms/call, {B * T / (ms * 1e-3) / 1e6:.3f} M tok/s, "
+              f"{flop / (ms * 1e-3) / 1e12:.1f} TFLOP/s (recurrent form)", flush=True)
+        del x, v, ctx, rho
+    return {"metric": METRIC + " [fp32 path]", "value": out["c1"]["tokens_per_s"], "unit": "tokens/s",
+            "steps": max(5, args.steps), "warmup": 3, "ms_per_step": out["c1"]["ms_per_call"],
+            "config": {"workload": "fp32 path through the reference surface: C1 in full, and the C2 "
+                                   "shape in fp32 under 'c2_shape'", "global_batch": 1, "seq_len": 256,
+                                   "parallelism": "single-gpu"},
+            "dtype": "f32", **out}
+
+
+def bench_rmw(torch):
+    """HBM ceilings on a 2 GiB buffer (C3's rho: 64 x 4 x 8192 rows of 1 KiB):
+    a read, a copy, an in-place read-modify-write, and a read-modify-write of
+    5 % / 10 % of the 1 KiB rows picked at random (sorted, as a decode step
+    walks each stream's active rows), through bdh_calib_hbm.  Bytes moved: read
+    = size, copy and RMW = 2 x size, row RMW = 2 x rows x 1 KiB."""
+    import numpy as np
+    from burn_dragon_amd import _lib
+    lib = _lib.load()
+    nbytes = 64 * 4 * 8192 * 1024
+    a = torch.zeros(nbytes // 4, device="cuda", dtype=torch.float32)
+    b = torch.empty_like(a)
+    sink = torch.zeros(4, device="cuda", dtype=torch.float32)
+    total_rows = nbytes // 1024
+    rng = np.random.default_rng(SEED + 9)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    out = {"buffer_bytes": nbytes}
+
+    def run(name, kind, buf2, rows, moved):
+        n_rows = 0 if rows is None else rows.numel()
+        call = lambda: lib.bdh_calib_hbm(kind, p(a), buf2, nbytes, p(rows) if rows is not None else None,  # noqa: E731
+                                         n_rows, stream)
+        for _ in range(2):
+            if call() != 0:
+                raise RuntimeError(_lib.last_error())
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[name] = {"us": round(ms * 1e3, 2), "bytes": moved, "GBs": round(moved / (ms * 1e-3) / 1e9, 1)}
+        print(f"[rmw] {name}: {ms * 1e3:.1f} us, {moved / (ms * 1e-3) / 1e12:.2f} TB/s", flush=True)
+
+    run("read", _lib.BDH_CALIB_READ, p(sink), None, nbytes)
+    run("copy", _lib.BDH_CALIB_COPY, p(b), None, 2 * nbytes)
+    run("rmw", _lib.BDH_CALIB_RMW, None, None, 2 * nbytes)
+    for pct in (5, 10):
+        pick = np.sort(rng.choice(total_rows, total_rows * pct // 100, replace=False)).astype(np.int32)
+        rows = torch.from_numpy(pick).cuda()
+        run(f"rmw_rows_{pct}pct", _lib.BDH_CALIB_RMW_ROWS, None, rows, 2 * pick.size * 1024)
+    print(json.dumps({"calibration": "hbm", **out}), flush=True)
+
+
 # --------------------------------------------------------------------------- #
 def main():
     args = parse()
@@ -537,11 +685,15 @@ def main():
     if args.only == "copy":
         bench_copy(torch)
         return
+    if args.only == "rmw":
+        bench_rmw(torch)
+        return
     pre = bench_prefill(torch, args) if args.only in ("all", "prefill") else None
     dec = bench_decode(torch, args) if args.only in ("all", "decode") else None
     lng = bench_long(torch, args) if args.only in ("all", "long") else None
     mdl = bench_model(torch, args) if args.only in ("all", "model") else None
     mdd = bench_model_decode(torch, args) if args.only in ("all", "model-decode") else None
+    f32 = bench_f32(torch, args) if args.only in ("all", "f32") else None
 
     cpu_pre = cpu_dec = None
     if not args.no_cpu_baseline:
@@ -577,10 +729,13 @@ def main():
             out["model"] = mdl
         if mdd is not None:
             out["model_decode"] = mdd
+        if f32 is not None:
+            out["fp32_path"] = f32
     elif dec is None:
-        one = next(r for r in (lng, mdl, mdd) if r is not None)
+        one = next(r for r in (lng, mdl, mdd, f32) if r is not None)
         out = dict(one, n_gpus=1, higher_is_better=True, scaling="weak", vs_baseline=None,
-                   dtype="bf16", data="synthetic")
+                   data="synthetic")
+        out.setdefault("dtype", "bf16")
     else:
         out = {"metric": METRIC, "value": round(dec["value"], 1), "unit": "tokens/s", "n_gpus": 1,
                "steps": dec["steps"], "warmup": dec["warmup"],

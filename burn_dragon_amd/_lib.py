@@ -22,6 +22,7 @@ BDH_F32 = 0
 BDH_BF16 = 1
 
 BDH_KERNEL_PREFILL, BDH_KERNEL_DECODE = 0, 1
+BDH_CALIB_READ, BDH_CALIB_COPY, BDH_CALIB_RMW, BDH_CALIB_RMW_ROWS = 0, 1, 2, 3
 BDH_ROPE_SEQUENTIAL = 0
 BDH_ROPE_FIXED = 1
 
@@ -94,6 +95,7 @@ SIGNATURES = {
                                       ctypes.POINTER(ctypes.c_int64)]),
     "bdh_scratch_release": (_i32, [_vp]),
     "bdh_selftest_rot8": (_i32, [_vp] * 6 + [_i64, _vp]),
+    "bdh_calib_hbm": (_i32, [_i32, _vp, _vp, _i64, _vp, _i64, _vp]),
     "bdh_last_error": (ctypes.c_char_p, []),
     "bdh_version": (ctypes.c_char_p, []),
 }

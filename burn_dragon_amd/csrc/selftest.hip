@@ -62,3 +62,94 @@ extern "C" bdh_status bdh_selftest_rot8(const void* x, const void* cs, void* out
   BDH_HIP_TRY(hipGetLastError());
   return BDH_OK;
 }
+
+// ---------------------------------------------------------------------------
+// HBM calibration kernels: the ceilings a decode step is compared against.
+// A decode step reads and rewrites scattered 1 KiB rows of rho (one row per
+// active neuron), which is neither a read nor a copy; these measure plain
+// streams and a row RMW of the same granularity on this device.
+namespace bdh {
+namespace {
+
+constexpr int kCalibBlock = 256;
+
+__global__ __launch_bounds__(kCalibBlock) void calib_read_kernel(const float4* __restrict__ a,
+                                                                 float* __restrict__ sink, int64_t n) {
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t i = (int64_t)blockIdx.x * kCalibBlock + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kCalibBlock) {
+    const float4 v = a[i];
+    s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+  }
+  // Never true for finite data; keeps the loads live without a store per thread.
+  if (s.x == 1.5e38f && s.y == -1.5e38f) sink[0] = s.z + s.w;
+}
+
+__global__ __launch_bounds__(kCalibBlock) void calib_copy_kernel(const float4* __restrict__ a,
+                                                                 float4* __restrict__ b, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kCalibBlock + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kCalibBlock)
+    b[i] = a[i];
+}
+
+__global__ __launch_bounds__(kCalibBlock) void calib_rmw_kernel(float4* __restrict__ a, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kCalibBlock + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kCalibBlock) {
+    float4 v = a[i];
+    v.x += 1.0f;
+    a[i] = v;
+  }
+}
+
+// One wavefront per listed 1 KiB row (64 lanes x 16 B), rows taken in list
+// order; an index outside [0, total_rows) is skipped.
+__global__ __launch_bounds__(kCalibBlock) void calib_rmw_rows_kernel(float4* __restrict__ a,
+                                                                     const int32_t* __restrict__ rows,
+                                                                     int64_t n_rows, int64_t total_rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * (kCalibBlock / 64);
+  for (int64_t r = (int64_t)blockIdx.x * (kCalibBlock / 64) + (threadIdx.x >> 6); r < n_rows; r += waves) {
+    const int64_t row = rows[r];
+    if (row < 0 || row >= total_rows) continue;
+    float4* p = a + row * 64 + lane;
+    float4 v = *p;
+    v.x += 1.0f;
+    *p = v;
+  }
+}
+
+}  // namespace
+}  // namespace bdh
+
+extern "C" bdh_status bdh_calib_hbm(int32_t kind, void* buf, void* buf2, int64_t bytes,
+                                    const int32_t* rows, int64_t n_rows, void* stream) {
+  if (!buf || bytes <= 0 || (bytes & 1023) != 0) return fail(BDH_EINVAL, "bytes must be a positive multiple of 1024");
+  if (((uintptr_t)buf & 15) != 0 || (buf2 && ((uintptr_t)buf2 & 15) != 0))
+    return fail(BDH_EINVAL, "buffers must be 16-byte aligned");
+  const int64_t n = bytes / 16;
+  const hipStream_t st = (hipStream_t)stream;
+  // 8 workgroups of 256 per CU on the 256 CUs; grid-stride loops cover the rest.
+  const dim3 grid(2048), block(kCalibBlock);
+  switch (kind) {
+    case BDH_CALIB_READ:
+      if (!buf2) return fail(BDH_EINVAL, "read needs a 16-byte sink in buf2");
+      hipLaunchKernelGGL(calib_read_kernel, grid, block, 0, st, (const float4*)buf, (float*)buf2, n);
+      break;
+    case BDH_CALIB_COPY:
+      if (!buf2) return fail(BDH_EINVAL, "copy needs a destination in buf2");
+      hipLaunchKernelGGL(calib_copy_kernel, grid, block, 0, st, (const float4*)buf, (float4*)buf2, n);
+      break;
+    case BDH_CALIB_RMW:
+      hipLaunchKernelGGL(calib_rmw_kernel, grid, block, 0, st, (float4*)buf, n);
+      break;
+    case BDH_CALIB_RMW_ROWS:
+      if (!rows || n_rows <= 0) return fail(BDH_EINVAL, "rmw_rows needs row indices");
+      hipLaunchKernelGGL(calib_rmw_rows_kernel, grid, block, 0, st, (float4*)buf, rows, n_rows,
+                         bytes / 1024);
+      break;
+    default:
+      return fail(BDH_EINVAL, "unknown calibration kind");
+  }
+  BDH_HIP_TRY(hipGetLastError());
+  return BDH_OK;
+}

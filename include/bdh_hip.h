@@ -335,6 +335,25 @@ bdh_status bdh_selftest_rot8(const void* x, const void* cs, void* out_bf16_asm,
                              void* out_bf16_builtin, float* out_f32_asm, float* out_f32_builtin,
                              int64_t n_chunks, void* stream);
 
+/* HBM calibration hook, no counterpart in the reference: one launch of a
+ * plain bandwidth kernel over `bytes` (a multiple of 1024) of device memory,
+ * the ceilings the decode step's bytes per second are read against.
+ *   BDH_CALIB_READ      read buf (buf2: a 16-byte sink, never written for
+ *                       finite data)
+ *   BDH_CALIB_COPY      buf -> buf2
+ *   BDH_CALIB_RMW       buf[i] += (1, 0, 0, 0) in place
+ *   BDH_CALIB_RMW_ROWS  the same on the 1 KiB rows rows[0..n_rows) of buf,
+ *                       one wavefront per row; indices outside
+ *                       [0, bytes / 1024) are skipped. */
+typedef enum {
+  BDH_CALIB_READ = 0,
+  BDH_CALIB_COPY = 1,
+  BDH_CALIB_RMW = 2,
+  BDH_CALIB_RMW_ROWS = 3
+} bdh_calib_kind;
+bdh_status bdh_calib_hbm(int32_t kind, void* buf, void* buf2, int64_t bytes, const int32_t* rows,
+                         int64_t n_rows, void* stream);
+
 /* Thread-local message of the last non-OK status of this thread. */
 const char* bdh_last_error(void);
 

@@ -302,3 +302,41 @@ double bdh_oracle_ndarray_recurrent_f32(const float* q, const float* v,
   }
   return omp_get_wtime() - t0;
 }
+
+/* CPU baseline, dense-score form without state or decay: the NdArray op
+ * sequence of linear.rs:241 and 321 with its [T, T] temporary materialised,
+ * scores = (Q Q^T).tril(-1), context = scores V, fp32, OpenMP over (b, h).
+ * Returns the wall time in seconds. */
+double bdh_oracle_ndarray_dense_f32(const float* q, const float* v, int64_t B,
+                                    int64_t H, int64_t Hv, int64_t T, int64_t N,
+                                    int64_t D, float* ctx_out, int32_t threads) {
+  if (threads > 0) omp_set_num_threads(threads);
+  double t0 = omp_get_wtime();
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t b = 0; b < B; ++b) {
+    for (int64_t h = 0; h < H; ++h) {
+      const float* Q = q + (b * H + h) * T * N;
+      const float* V = v + (b * Hv + vhead(Hv, h)) * T * D;
+      float* C = ctx_out + (b * H + h) * T * D;
+      float* S = (float*)malloc(sizeof(float) * (size_t)(T * T));
+      for (int64_t r = 0; r < T; ++r)
+        for (int64_t c = 0; c < T; ++c) {
+          float s = 0.0f;
+          for (int64_t l = 0; l < N; ++l) s += Q[r * N + l] * Q[c * N + l];
+          S[r * T + c] = s;
+        }
+      for (int64_t r = 0; r < T; ++r)           /* tril(-1) */
+        for (int64_t c = r; c < T; ++c) S[r * T + c] = 0.0f;
+      for (int64_t r = 0; r < T; ++r) {
+        float* cr = C + r * D;
+        for (int64_t e = 0; e < D; ++e) cr[e] = 0.0f;
+        for (int64_t c = 0; c < T; ++c) {
+          const float s = S[r * T + c];
+          for (int64_t e = 0; e < D; ++e) cr[e] += s * V[c * D + e];
+        }
+      }
+      free(S);
+    }
+  }
+  return omp_get_wtime() - t0;
+}

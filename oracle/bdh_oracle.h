@@ -94,6 +94,13 @@ double bdh_oracle_ndarray_recurrent_f32(const float* q, const float* v,
                                         float* ctx_out, float* rho_out,
                                         int32_t threads);
 
+/* CPU baseline, dense-score form (linear.rs:241, 321) without state or
+ * decay: scores = (Q Q^T).tril(-1) materialised as [T, T], context =
+ * scores V, fp32, OpenMP over (b,h).  Returns wall seconds. */
+double bdh_oracle_ndarray_dense_f32(const float* q, const float* v, int64_t B,
+                                    int64_t H, int64_t Hv, int64_t T, int64_t N,
+                                    int64_t D, float* ctx_out, int32_t threads);
+
 #ifdef __cplusplus
 }
 #endif

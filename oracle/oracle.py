@@ -50,6 +50,8 @@ def lib():
         L.bdh_oracle_ndarray_recurrent_f32.argtypes = [_f32p, _f32p, _f32p, _f32p] + [_i64] * 6 + [
             _f32p, _f32p, ctypes.c_int32]
         L.bdh_oracle_ndarray_recurrent_f32.restype = ctypes.c_double
+        L.bdh_oracle_ndarray_dense_f32.argtypes = [_f32p, _f32p] + [_i64] * 6 + [_f32p, ctypes.c_int32]
+        L.bdh_oracle_ndarray_dense_f32.restype = ctypes.c_double
         _lib = L
     return _lib
 
@@ -186,6 +188,18 @@ def ndarray_recurrent_f32(q, v, rho0=None, decay=None, threads: int = 0):
                                                   ctx.ctypes.data_as(_f32p),
                                                   rho.ctypes.data_as(_f32p), threads)
     return ctx, rho, secs
+
+
+def ndarray_dense_f32(q, v, threads: int = 0):
+    """CPU baseline, dense-score form without state or decay: the NdArray op
+    sequence of linear.rs:241, 321 ((Q Q^T).tril(-1) materialised, then
+    scores V), fp32, OpenMP over (b, h).  Returns (ctx, wall_seconds)."""
+    q, qp = _f32(q)
+    v, vp = _f32(v)
+    B, H, Hv, T, N, D = _dims(q, v)
+    ctx = np.empty((B, H, T, D), np.float32)
+    secs = lib().bdh_oracle_ndarray_dense_f32(qp, vp, B, H, Hv, T, N, D, ctx.ctypes.data_as(_f32p), threads)
+    return ctx, secs
 
 
 def layer_norm_f64(x, eps: float = 1e-5) -> np.ndarray:

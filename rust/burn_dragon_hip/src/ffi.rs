@@ -17,6 +17,10 @@ pub const BDH_ROPE_SEQUENTIAL: i32 = 0;
 pub const BDH_ROPE_FIXED: i32 = 1;
 pub const BDH_KERNEL_PREFILL: i32 = 0;
 pub const BDH_KERNEL_DECODE: i32 = 1;
+pub const BDH_CALIB_READ: i32 = 0;
+pub const BDH_CALIB_COPY: i32 = 1;
+pub const BDH_CALIB_RMW: i32 = 2;
+pub const BDH_CALIB_RMW_ROWS: i32 = 3;
 
 #[repr(C)]
 #[derive(Clone, Copy, Debug, Default)]
@@ -147,6 +151,8 @@ extern "C" {
     pub fn bdh_selftest_rot8(x: *const c_void, cs: *const c_void, out_bf16_asm: *mut c_void,
                              out_bf16_builtin: *mut c_void, out_f32_asm: *mut f32,
                              out_f32_builtin: *mut f32, n_chunks: i64, stream: *mut c_void) -> i32;
+    pub fn bdh_calib_hbm(kind: i32, buf: *mut c_void, buf2: *mut c_void, bytes: i64,
+                         rows: *const i32, n_rows: i64, stream: *mut c_void) -> i32;
     pub fn bdh_last_error() -> *const c_char;
     pub fn bdh_version() -> *const c_char;
 }

@@ -72,6 +72,49 @@ def test_profile_counts_calls_and_launches():
     assert snap.calls == 3 and snap.launches >= 9 and snap.total_ns > 0
 
 
+def test_profile_allocation_metadata_and_rollout_counters():
+    """The counters recurrent.rs:206-215, 344-356 fills: a first call of a
+    (latent, theta) no other test uses uploads its RoPE table and allocates;
+    the same call again allocates nothing and finds the table resident; a
+    T = 1 in-place fp32 step counts one resident rollout step; copy_ns stays 0
+    (the private rho copy is fused into the kernel writing rho_out)."""
+    torch = need_gpu()
+    import ctypes
+    import burn_dragon_amd as bd
+    from burn_dragon_amd import _lib
+    N, D, theta = 24, 8, 777.25
+    rng = np.random.default_rng(31)
+    x = dev(torch, rc.sparse_relu(rng, (1, 2, 3, N)))
+    v = dev(torch, rc.gaussian(rng, (1, 1, 3, D)))
+    x1 = dev(torch, rc.sparse_relu(rng, (1, 2, 1, N)))
+    v1 = dev(torch, rc.gaussian(rng, (1, 1, 1, D)))
+    side = torch.cuda.Stream()  # a fresh stream: its scratch starts empty
+    side.wait_stream(torch.cuda.current_stream())
+    announce("api profile counters")
+    bd.recurrent_profile_enable(True)
+    try:
+        with torch.cuda.stream(side):
+            bd.recurrent_profile_reset()
+            out = bd.try_fused_recurrent_attention_rope(x, v, theta=theta)
+            s1 = bd.recurrent_profile_snapshot()
+            out = bd.try_fused_recurrent_attention_rope(x, v, theta=theta)
+            s2 = bd.recurrent_profile_snapshot()
+            rho = out.rho.clone()
+            bd.try_fused_recurrent_attention_rope(x1, v1, rho, position=3, theta=theta, inplace=True)
+            s3 = bd.recurrent_profile_snapshot()
+        side.synchronize()
+    finally:
+        bd.recurrent_profile_enable(False)
+        assert _lib.load().bdh_scratch_release(ctypes.c_void_p(side.cuda_stream)) == _lib.BDH_OK
+    assert s1.calls == 1 and s1.transient_allocations >= 1
+    assert s1.metadata_upload_bytes == 4 * N and s1.metadata_reuse_hits == 0
+    assert s2.calls == 2 and s2.transient_allocations == s1.transient_allocations
+    assert s2.metadata_reuse_hits == 1 and s2.metadata_reuse_bytes == 4 * N
+    assert s2.metadata_upload_bytes == 4 * N
+    assert s3.calls == 3 and s3.resident_rollout_steps == 1
+    assert s3.copy_ns == 0 and s3.setup_ns > 0 and s3.dispatch_ns > 0
+
+
 def test_memory_stays_bounded_across_repeated_calls():
     # recurrent/tests.rs:290-336: 32 calls carrying rho must not grow memory.
     torch = need_gpu()

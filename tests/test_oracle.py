@@ -137,6 +137,20 @@ def test_f32_mirror_matches_ndarray_baseline_bitwise(oracle):
     assert np.array_equal(c1, c2) and np.array_equal(r1, r2)
 
 
+def test_dense_score_baseline_matches_numpy_closed_form(oracle):
+    """The dense-score CPU baseline (fp32, [T, T] scores materialised)
+    against the f64 numpy closed form, C1's distributions at a reduced size,
+    per-head and shared values; a dropped tril (diagonal kept) fails."""
+    rng = np.random.default_rng(17)
+    q = oracle.rope_rotate(rc.sparse_relu(rng, (1, 4, 64, 256)))
+    for v in (rc.gaussian(rng, (1, 1, 64, 32)), rc.gaussian(rng, (1, 4, 64, 32))):
+        ctx, secs = oracle.ndarray_dense_f32(q, v, threads=2)
+        want, _ = closed_form_np(q, v)
+        assert oracle.rel_l2(ctx, want) < 1e-6 and secs >= 0.0
+        diag, _ = closed_form_np(q, v, include_diag=True)
+        assert oracle.rel_l2(ctx, diag) > 1e-2
+
+
 # --- RoPE -------------------------------------------------------------------
 
 def test_rope_freqs_closed_form(oracle):
