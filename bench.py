@@ -136,6 +136,8 @@ def bench_prefill(torch, args):
     # replayed: the deployment form of a fixed-shape prefill, without the
     # host launch gaps.  Every replay recomputes ctx and rho in full; the
     # replays are checked bit for bit against the eager result first.
+    # The library keeps its scratch per stream and cannot grow it during a
+    # capture, so the capture runs on a stream that made one eager call.
     ref_ctx, ref_rho = ctx.clone(), rho.clone()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -143,7 +145,7 @@ def bench_prefill(torch, args):
         lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho)
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho)
     for _ in range(3):
         ctx.zero_()
@@ -187,7 +189,7 @@ def bench_prefill(torch, args):
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": TRAFFIC_PREFILL_C2, "kernel": "prefill_mfma_kernel",
                      "kernel_avg_us": round(k_ms / k_n * 1e3, 2), "flop_per_launch": k_flop / k_n,
-                     "pass": {"kernels": "prep_bf16_kernel + prefill_mfma_kernel + ctx_kernel",
+                     "pass": {"kernels": "transpose_v_kernel + prefill_mfma_kernel + ctx_kernel",
                               "event_ms": round(ev_ms, 4), "tflops": round(pass_tflops, 2),
                               "flop": flop, "traffic": TRAFFIC_PREFILL_C2_PASS}},
         "shape": {"B": B, "nh": H, "T": T, "N": N, "D": D, "chunk": C},
@@ -327,14 +329,24 @@ def bench_decode(torch, args):
 
 # --------------------------------------------------------------------------- #
 def _cpu_model() -> str:
+    """Model name of the host CPU with its family / model / stepping numbers
+    (a virtual machine may report only a generic name)."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return f"{line.split(':', 1)[1].strip()} ({os.cpu_count()} logical CPUs visible)"
+                if ":" in line:
+                    k, v = (t.strip() for t in line.split(":", 1))
+                    if k in ("model name", "cpu family", "model", "stepping") and k not in info:
+                        info[k] = v
+                if not line.strip() and info:
+                    break
     except OSError:
         pass
-    return f"unknown ({os.cpu_count()} logical CPUs visible)"
+    name = info.get("model name", "unknown")
+    ids = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info)
+    return f"{name} ({ids}; {os.cpu_count()} logical CPUs visible)" if ids else \
+        f"{name} ({os.cpu_count()} logical CPUs visible)"
 
 
 def cpu_baseline_prefill(target_s: float):

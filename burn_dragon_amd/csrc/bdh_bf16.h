@@ -19,7 +19,7 @@ __device__ __forceinline__ uint4 ldg16_off(const void* base, uint32_t byte_off) 
 }
 
 // RoPE rotation of 4 (even, odd) bf16 pairs x.{x,y,z,w} by the packed bf16
-// (cos, sin) words cs.{x,y,z,w}:
+// (cos, sin) words cs.{x,y,z,w} (rope_cs4 below):
 //   re = e*c - o*s = (e, o) . (c, s) with the high product negated (neg_hi)
 //   ro = o*c + e*s = (o, e) . (c, s), (o, e) = x rotated by 16 bits
 // Written in assembly for the three-operand v_dot2_f32_bf16 and its neg_hi
@@ -140,7 +140,9 @@ __device__ __forceinline__ float decay_pow_int(float d, float l2a, int e) {
 // Any kind may be absent (gram_ids, rd_units or state_units == 0).
 struct PrefillArgs {
   const bf16_t* x;      // [S, T, N]
-  const uint32_t* cs;   // packed bf16 (cos, sin) [T, N/2], or null (x pre-rotated)
+  const float* freqs;   // RoPE frequencies [N] (rotating kernels), or null (x pre-rotated)
+  int64_t pos0;         // position of token 0 (Sequential), or of every token (fixed)
+  int fixed;
   const float* decay;   // [H] or null
   int64_t H, Hv, T, N, D, S;
   // gram units
@@ -170,11 +172,35 @@ struct PrefillArgs {
   float* add_ctx;       // [S, T, D]
   int64_t add_t0, add_Lc;
   int add_units;
-  // table_key, if set: workgroup 0 writes table_key_val there (the key of
-  // the (cos, sin) table this launch reads)
-  int64_t* table_key;
-  int64_t table_key_val[6];
 };
+
+// RoPE position of token t of the call (attention.rs:488-501 with the
+// Sequential or Fixed positions of the call): exact in f32 below 2^24.
+__device__ __forceinline__ float rope_pos(const PrefillArgs& a, int64_t t) {
+  return (float)(a.fixed ? a.pos0 : a.pos0 + t);
+}
+// Frequencies of the 4 (even, odd) pairs of 8 neurons starting at f (one per
+// pair: the even neuron's; 16-byte aligned).
+__device__ __forceinline__ void load_freq4(const float* f, float (&out)[4]) {
+  const float4 a = *reinterpret_cast<const float4*>(f);
+  const float4 b = *reinterpret_cast<const float4*>(f + 4);
+  out[0] = a.x;
+  out[1] = a.z;
+  out[2] = b.x;
+  out[3] = b.z;
+}
+// Packed bf16 (cos, sin) words of the 4 pairs at position p: the phase
+// frac(p f) in the reference's f32 op order; v_cos_f32 / v_sin_f32 take
+// their argument in revolutions (error ~1e-6, far below the bf16 rounding).
+__device__ __forceinline__ uint4 rope_cs4(float p, const float (&f)[4]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float fr = rope_frac(p, f[j]);
+    w[j] = pack_bf16x2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
 // Workgroup ids a gram launch needs for `groups` groups of nb-block
 // intervals (ids are laid out so that one group's tiles share an XCD).

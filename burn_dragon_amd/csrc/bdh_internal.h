@@ -26,7 +26,6 @@ bdh_status hip_fail(hipError_t e, const char* what);
 enum ScratchSlot {
   SLOT_SCORES = 0,   // causal score partials    [KS, S, n_iv, Lp, Lp] f32
   SLOT_VT,           // transposed values        [B*Hv, Dp, Tp] bf16
-  SLOT_ROPE_TABLE,   // table key (8 int64), then packed bf16 cos/sin per (token, pair) [T, N/2]
   SLOT_ROTATED,      // rotated queries [S, T, N]: f32 (fp32 path) or bf16 (bf16 path)
   SLOT_READOUT,      // readout partials (bf16 path) [rd_kr, S, Lp, D] f32
   SLOT_RHO_A,        // states between intervals (bf16 path) [S, N, D] f32

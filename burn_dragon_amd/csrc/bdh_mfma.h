@@ -157,6 +157,7 @@ __device__ __forceinline__ void dma_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+
 // acc += A x B^T over one 32-deep step, as mma_64x128, with the fragment LDS
 // reads in assembly: used where the LDS holds direct-load stages, so that
 // the compiler (which cannot tell them apart from the DMAs in flight) does
@@ -200,54 +201,6 @@ __device__ __forceinline__ void mma_64x128_dsasm(const bf16_t* A, const bf16_t* 
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
     for (int ni = 4; ni < 8; ++ni) mm(mi, ni);
-}
-
-// Register-set index of a two-set stage, as a compile-time constant.
-template <int S>
-using Set = std::integral_constant<int, S>;
-
-// As run_steps, for operands rotated by RoPE from a (cos, sin) table: the
-// table words of a 16-byte x chunk are only fetched when the chunk is
-// nonzero (ReLU activations leave most chunks zero), so x must be in
-// registers before its table loads are issued.  x of step kt is loaded two
-// steps ahead into register set (kt - kb) & 1, the table (and any other
-// operand) one step ahead, masked by that x; store(buf, set) rotates set's
-// step and writes it to LDS buffer buf.  Steps [kb, ke), an even count >= 2.
-template <class LoadX, class LoadT, class Store, class Compute>
-__device__ __forceinline__ void run_steps_x2(int kb, int ke, LoadX&& loadx, LoadT&& loadt,
-                                             Store&& store, Compute&& compute) {
-  loadx(kb, Set<0>{});
-  loadx(kb + 1, Set<1>{});
-  loadt(kb, Set<0>{});
-  store(0, Set<0>{});
-  __syncthreads();
-  for (int kt = kb; kt < ke; kt += 2) {
-    loadt(kt + 1, Set<1>{});
-    if (kt + 2 < ke) loadx(kt + 2, Set<0>{});
-    compute(0);
-    store(1, Set<1>{});
-    __syncthreads();
-    if (kt + 2 < ke) {
-      loadt(kt + 2, Set<0>{});
-      if (kt + 3 < ke) loadx(kt + 3, Set<1>{});
-    }
-    compute(1);
-    if (kt + 2 < ke) store(0, Set<0>{});
-    __syncthreads();
-  }
-}
-
-// True when any of the 8 bf16 of a chunk is nonzero (the sign bit ignored).
-__device__ __forceinline__ bool chunk_nonzero(uint4 x) {
-  return ((x.x | x.y | x.z | x.w) & 0x7fff7fffu) != 0;
-}
-
-// 16-byte table load for a nonzero x chunk; zeros otherwise (the rotation of
-// a zero chunk is zero whatever the table holds).
-__device__ __forceinline__ uint4 ldg16_if(bool on, const void* base, uint32_t byte_off) {
-  uint4 t = make_uint4(0, 0, 0, 0);
-  if (on) t = ldg16_off(base, byte_off);
-  return t;
 }
 
 }  // namespace mfma

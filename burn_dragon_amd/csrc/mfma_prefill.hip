@@ -18,8 +18,9 @@
 //               range (split-K partial); rho is read as fp32 rows and
 //               written transposed as bf16 to LDS.
 //
-// q = RoPE(x) is applied between HBM and LDS from the packed bf16 (cos, sin)
-// table.  K steps are 32 deep; LDS holds two steps (double buffer) and the
+// q = RoPE(x) is applied between HBM and LDS: each lane computes the packed
+// bf16 (cos, sin) words of its 4 pairs from the f32 phase frac(p f) (v_cos /
+// v_sin take revolutions) and rotates with v_dot2.  K steps are 32 deep; LDS holds two steps (double buffer) and the
 // global loads of step k+1 are in flight while step k is multiplied.  Every
 // unit runs an even number of steps (the host guarantees it), so the step
 // loop has a single exit; with a mid-loop exit the compiler moves the
@@ -46,9 +47,8 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int64_t t0 = iv * a.L;
   const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
-  const int64_t rowb = a.N * 2;  // bytes per x row, and per table row (N/2 words)
+  const int64_t rowb = a.N * 2;  // bytes per x row
   const char* X = reinterpret_cast<const char*>(a.x + (s * a.T + t0) * a.N);
-  const char* CS = ROPE ? reinterpret_cast<const char*>(a.cs + t0 * (a.N / 2)) : nullptr;
   const int nk = (int)(a.N / BK);
   const int kb = (int)((int64_t)nk * kp / a.ks), ke = (int)((int64_t)nk * (kp + 1) / a.ks);
 
@@ -68,9 +68,9 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   const int kc = tid & 3, rb = tid >> 2;
   const uint32_t lane_off = (uint32_t)(rb * rowb + kc * 16);
   // Uniform base and per-lane offset of group g's 16 bytes of step kt in a
-  // [token][N] array (x, or the table, whose rows have the same byte pitch).
+  // [token][N] array.
   auto at = [&](int g, int kt, uint32_t& off) -> int64_t {
-    const int64_t kofs = (int64_t)kt * 64;  // 32 bf16 of x, 16 words of the table
+    const int64_t kofs = (int64_t)kt * 64;  // 32 bf16 of x
     const int64_t r0 = PAIR ? (g < 2 ? ri + 64 * g : rj2 + 64 * (g - 2))
                             : (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
     if (WHOLE) {
@@ -81,37 +81,16 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
     off = (uint32_t)((t < Lc ? t : Lc - 1) * rowb + kc * 16);
     return kofs;
   };
-  struct Stage {
-    uint4 xr[2][6], cr[6];
-  } st;
-  auto loadx = [&](int kt, auto set) {
+  // RoPE: the position of each group's row for this lane (constant over the
+  // steps) and the step's 4 pair frequencies (neurons 32 kt + 8 kc + 2 j).
+  float pg[6];
 #pragma unroll
-    for (int g = 0; g < 6; ++g) {
-      if (g >= groups) break;
-      uint32_t off;
-      const int64_t o = at(g, kt, off);
-      st.xr[decltype(set)::value][g] = ldg16_off(X + o, off);
-    }
-  };
-  auto loadt = [&](int kt, auto set) {
-#pragma unroll
-    for (int g = 0; g < 6; ++g) {
-      if (g >= groups) break;
-      uint32_t off;
-      const int64_t o = at(g, kt, off);
-      st.cr[g] = ldg16_if(chunk_nonzero(st.xr[decltype(set)::value][g]), CS + o, off);
-    }
-  };
-  auto store = [&](int buf, auto set) {
-    bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
-#pragma unroll
-    for (int g = 0; g < 6; ++g) {
-      if (g >= groups) break;
-      *reinterpret_cast<uint4*>(&base[lds_off(64 * g + rb, kc)]) =
-          prep8<ROPE>(st.xr[decltype(set)::value][g], st.cr[g], 1.0f, false);
-    }
-  };
-
+  for (int g = 0; g < 6; ++g) {
+    const int64_t r0 = PAIR ? (g < 2 ? ri + 64 * g : rj2 + 64 * (g - 2))
+                            : (g < 4 ? ri + 64 * g : rj + 64 * (g - 4));
+    const int64_t t = WHOLE ? r0 + rb : (r0 + rb < Lc ? r0 + rb : Lc - 1);
+    pg[g] = ROPE ? rope_pos(a, t0 + t) : 0.0f;
+  }
   floatx4 acc[4][8];
   zero_acc(acc);
   // Waves whose 64 rows end at or before the tile's first column compute
@@ -121,9 +100,6 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   const int64_t wr0 = PAIR ? wc0 + 64 * (w & 1) : ri + 64 * w;
   const bool active = PAIR ? (wr0 < Lc && (w < 2 || rj >= 0)) : (wr0 + 64 > rj + 1 && wr0 < Lc);
   const int brow = PAIR ? 128 * (w >> 1) : inner ? (int)(rj - ri) : T256;  // LDS row of the first B row
-  auto compute = [&](int buf) {
-    if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF, lane, 64 * w, brow, acc);
-  };
   if (!ROPE) {
     // Operands need no rotation: a three-stage LDS ring filled by direct
     // loads two steps ahead, one barrier per step, no register staging.
@@ -175,25 +151,37 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
       stg = stg == 2 ? 0 : stg + 1;
     }
     dma_wait_barrier<0>();  // the epilogue reuses the ring
-  } else if (ROPE && inner) {
-    // Two x sets of 4 chunks fit the register budget beside the
-    // accumulators; outer tiles (6 chunks) load x and the whole table one
-    // step ahead.
-    run_steps_x2(kb, ke, loadx, loadt, store, compute);
   } else {
-    run_steps(kb, ke,
-              [&](int kt) {
-                loadx(kt, Set<0>{});
-                if (ROPE) {
+    // RoPE: x and the step's frequencies one step ahead in registers; each
+    // thread rotates its chunks (phases computed per row) as it writes them
+    // to LDS.  (Rotating in place in a direct-load ring was slower: the
+    // rotation's VALU work, not the loads, bounds these steps.)
+    struct Stage {
+      uint4 xr[6];
+      float fq[4];
+    } st;
+    auto load = [&](int kt) {
 #pragma unroll
-                  for (int g = 0; g < groups; ++g) {
-                    uint32_t off;
-                    const int64_t o = at(g, kt, off);
-                    st.cr[g] = ldg16_off(CS + o, off);
-                  }
-                }
-              },
-              [&](int buf) { store(buf, Set<0>{}); }, compute);
+      for (int g = 0; g < 6; ++g) {
+        if (g >= groups) break;
+        uint32_t off;
+        const int64_t o = at(g, kt, off);
+        st.xr[g] = ldg16_off(X + o, off);
+      }
+      load_freq4(a.freqs + (int64_t)kt * BK + kc * 8, st.fq);
+    };
+    auto store = [&](int buf) {
+      bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
+#pragma unroll
+      for (int g = 0; g < 6; ++g) {
+        if (g >= groups) break;
+        *reinterpret_cast<uint4*>(&base[lds_off(64 * g + rb, kc)]) = rot8_bf16(st.xr[g], rope_cs4(pg[g], st.fq));
+      }
+    };
+    auto compute = [&](int buf) {
+      if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF, lane, 64 * w, brow, acc);
+    };
+    run_steps(kb, ke, load, store, compute);
   }
 
   // Scores of rows ti < Lc and columns tj < Lc: times d^(ti - tj) below
@@ -232,9 +220,8 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
   const int wm = w >> 1, wn = w & 1;  // n rows 64*wm.., d cols 128*wn..
   const int64_t b = s / a.H, h = s - b * a.H;
   const int64_t t0 = a.st_t0, Lc = a.st_Lc;
-  const int64_t rowb = a.N * 2;  // bytes per x row and per table row
+  const int64_t rowb = a.N * 2;  // bytes per x row
   const char* X = reinterpret_cast<const char*>(a.x + s * a.T * a.N);
-  const char* CS = reinterpret_cast<const char*>(a.cs);
   const char* VT = reinterpret_cast<const char*>(a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp);
   const float dk = DECAY ? a.decay[h] : 1.0f;
   const float l2d = DECAY ? decay_log2(dk) : 0.0f;
@@ -250,7 +237,7 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
   const int64_t vrow = a.Tp * 2;
   const uint32_t vlane = (uint32_t)(vb * vrow + kc * 16);
   // Uniform base and per-lane offset of token tb + i's 16 bytes for this
-  // lane in a [token][N] array (x, or the table: same byte pitch).
+  // lane in the [token][N] x.
   auto at = [&](int kt, int i, uint32_t& off) -> int64_t {
     const int64_t tb = t0 + (int64_t)kt * BK;
     if (WHOLE) {
@@ -261,46 +248,47 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
     off = (uint32_t)((t < a.T ? t : a.T - 1) * rowb + (n0 + 8 * nv) * 2);
     return 0;
   };
+  // RoPE: the lane's 4 pair frequencies are those of its 8 neurons, the same
+  // in every step.
+  float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (ROPE) load_freq4(a.freqs + n0 + 8 * nv, fq);
+  const float pbase = ROPE ? rope_pos(a, t0) : 0.0f;  // position of the interval's first token
   struct Stage {
-    uint4 xr[2][2], cr[2], vr[4];
+    uint4 xr[2], vr[4];
   } st;
-  int cur[2] = {0, 0};  // step held by each x set
-  auto loadx = [&](int kt, auto set) {
-    cur[decltype(set)::value] = kt;
+  int cur = 0;  // step held in st
+  auto load = [&](int kt) {
+    cur = kt;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       uint32_t off;
       const int64_t o = at(kt, i, off);
-      st.xr[decltype(set)::value][i] = ldg16_off(X + o, off);
+      st.xr[i] = ldg16_off(X + o, off);
     }
-  };
-  auto loadv = [&](int kt) {
     const int64_t tb = t0 + (int64_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < 4; ++i) st.vr[i] = ldg16_off(VT + (d0 + 64 * i) * vrow + tb * 2, vlane);
   };
-  auto loadt = [&](int kt, auto set) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t off;
-      const int64_t o = at(kt, i, off);
-      st.cr[i] = ldg16_if(chunk_nonzero(st.xr[decltype(set)::value][i]), CS + o, off);
-    }
-    loadv(kt);
-  };
-  auto store = [&](int buf, auto set) {
-    constexpr int S = decltype(set)::value;
+  auto store = [&](int buf) {
     bf16_t* A = lds + buf * BUF;             // [n][t], 128 rows
     bf16_t* B = lds + buf * BUF + 128 * BK;  // [d][t], 256 rows
     float f0[8], f1[8];
     float w0 = 1.0f, w1 = 1.0f;
+    const int64_t tl = (int64_t)cur * BK + 2 * tp;  // tokens tl, tl + 1 of the interval
     if (DECAY) {
-      const int64_t tl = (int64_t)cur[S] * BK + 2 * tp;
       w0 = tl < Lc ? decay_pow_int(dk, l2d, (int)(Lc - tl)) : 0.0f;
       w1 = tl + 1 < Lc ? decay_pow_int(dk, l2d, (int)(Lc - tl - 1)) : 0.0f;
     }
-    prep8_f32<ROPE>(st.xr[S][0], st.cr[0], w0, DECAY, f0);
-    prep8_f32<ROPE>(st.xr[S][1], st.cr[1], w1, DECAY, f1);
+    uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
+    if (ROPE) {
+      // Tokens past T (ragged last interval) add zero: any position will do.
+      // Sums of integers below 2^24 are exact in f32.
+      const float p0 = a.fixed ? pbase : pbase + (float)(int)tl;
+      c0 = rope_cs4(p0, fq);
+      c1 = rope_cs4(a.fixed ? pbase : p0 + 1.0f, fq);
+    }
+    prep8_f32<ROPE>(st.xr[0], c0, w0, DECAY, f0);
+    prep8_f32<ROPE>(st.xr[1], c1, w1, DECAY, f1);
     uint32_t* Aw = reinterpret_cast<uint32_t*>(A);
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -316,12 +304,7 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
   auto compute = [&](int buf) {
     if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF + 128 * BK, lane, 64 * wm, 128 * wn, acc);
   };
-  if (ROPE) {
-    run_steps_x2(0, nk, loadx, loadt, store, compute);
-  } else {
-    run_steps(0, nk, [&](int kt) { loadx(kt, Set<0>{}); loadv(kt); }, [&](int buf) { store(buf, Set<0>{}); },
-              compute);
-  }
+  run_steps(0, nk, load, store, compute);
 
   // Columns past D (zero v^T rows) are computed and never written; D is a
   // multiple of 32, so a float4 of columns is all in or all out.
@@ -359,9 +342,8 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
                                              int64_t r0, int64_t d0) {
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int64_t t0 = a.rd_t0, Lc = a.rd_Lc;
-  const int64_t rowb = a.N * 2;  // bytes per x row, and per table row (N/2 words)
+  const int64_t rowb = a.N * 2;  // bytes per x row
   const char* X = reinterpret_cast<const char*>(a.x + (s * a.T + t0) * a.N);
-  const char* CS = ROPE ? reinterpret_cast<const char*>(a.cs + t0 * (a.N / 2)) : nullptr;
   const float* R = a.rd_rho + s * a.N * a.D;
   const int nk = (int)(a.N / BK);
   const int kb = (int)((int64_t)nk * kp / a.rd_kr), ke = (int)((int64_t)nk * (kp + 1) / a.rd_kr);
@@ -372,32 +354,36 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
   // ragged interval re-read its last row and are never stored.
   const int kc = tid & 3, rb = tid >> 2;
   const uint32_t lane_off = (uint32_t)(rb * rowb + kc * 16);
-  float wr[4];
+  float wr[4], pg[4];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) wr[g] = DECAY ? decay_pow_int(dk, l2d, (int)(r0 + rb + 64 * g)) : 1.0f;
+  for (int g = 0; g < 4; ++g) {
+    wr[g] = DECAY ? decay_pow_int(dk, l2d, (int)(r0 + rb + 64 * g)) : 1.0f;
+    const int64_t t = r0 + 64 * g + rb;
+    pg[g] = ROPE ? rope_pos(a, t0 + (WHOLE || t < Lc ? t : Lc - 1)) : 0.0f;
+  }
   // rho loader: lane block of 2 state rows (2 np, 2 np + 1) x 8 columns
   // (8 dv ..); columns past D re-read the last 8 and are never stored.
   const int np = tid & 15, dv = tid >> 4;
   const int64_t dcol = d0 + 8 * dv <= a.D - 8 ? d0 + 8 * dv : a.D - 8;
   struct Stage {
-    uint4 xr[4], cr[4];
+    uint4 xr[4];
+    float fq[4];
     float4 rr[4];
   } st;
   auto load = [&](int kt) {
-    const int64_t kofs = (int64_t)kt * 64;  // 32 bf16 of x, 16 words of the table
+    const int64_t kofs = (int64_t)kt * 64;  // 32 bf16 of x
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       if (WHOLE) {
         const int64_t o = (r0 + 64 * g) * rowb + kofs;
         st.xr[g] = ldg16_off(X + o, lane_off);
-        if (ROPE) st.cr[g] = ldg16_off(CS + o, lane_off);
       } else {
         const int64_t t = r0 + 64 * g + rb;
         const uint32_t o = (uint32_t)((t < Lc ? t : Lc - 1) * rowb + kc * 16);
         st.xr[g] = ldg16_off(X + kofs, o);
-        if (ROPE) st.cr[g] = ldg16_off(CS + kofs, o);
       }
     }
+    if (ROPE) load_freq4(a.freqs + (int64_t)kt * BK + kc * 8, st.fq);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const float* row = R + ((int64_t)kt * BK + 2 * np + i) * a.D + dcol;
@@ -410,7 +396,8 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
     bf16_t* B = lds + buf * BUF + T256 * BK; // rho^T rows (columns d) 0..127
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<uint4*>(&A[lds_off(64 * g + rb, kc)]) = prep8<ROPE>(st.xr[g], st.cr[g], wr[g], DECAY);
+      *reinterpret_cast<uint4*>(&A[lds_off(64 * g + rb, kc)]) =
+          prep8<ROPE>(st.xr[g], ROPE ? rope_cs4(pg[g], st.fq) : make_uint4(0, 0, 0, 0), wr[g], DECAY);
     const float r0v[8] = {st.rr[0].x, st.rr[0].y, st.rr[0].z, st.rr[0].w,
                           st.rr[1].x, st.rr[1].y, st.rr[1].z, st.rr[1].w};
     const float r1v[8] = {st.rr[2].x, st.rr[2].y, st.rr[2].z, st.rr[2].w,
@@ -497,14 +484,6 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
   // Two register-path buffers, or the three-stage ring of the direct-load gram.
   __shared__ __attribute__((aligned(16))) bf16_t lds[3 * BUF];
   const int id = blockIdx.x;
-  // The table was complete before this launch began; name it for the next
-  // call's prep kernel.
-  // (Static indices: indexing the kernel argument by thread would copy it to
-  // private memory.)
-  if (a.table_key && id == 0 && threadIdx.x == 0) {
-#pragma unroll
-    for (int i = 0; i < 6; ++i) a.table_key[i] = a.table_key_val[i];
-  }
   if (id < a.gram_ids) {
     const int tpg = units_per_group(a.nb);
     const int blk = id / (8 * tpg), rem = id - blk * 8 * tpg;

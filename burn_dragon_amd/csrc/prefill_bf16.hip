@@ -15,9 +15,9 @@
 // gram, readout and state units share one launch per interval
 // (mfma_prefill.hip); the states between intervals alternate between two
 // scratch buffers and the last one lands in rho_out.
-// RoPE is applied to Q tiles between HBM and LDS from a packed bf16
-// (cos, sin) table of the call's (token, pair) phases; rotated queries are
-// never written to memory.
+// RoPE is applied to Q tiles between HBM and LDS, each lane computing the
+// (cos, sin) of its pairs from the f32 phase; with one interval rotated
+// queries are never written to memory.
 #include "bdh_bf16.h"
 
 namespace bdh {
@@ -268,59 +268,6 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const bf16_t* __restri
                    (int64_t)blockIdx.y * VT_TILE);
 }
 
-// Packed bf16 (cos, sin) of the RoPE phase of (token, pair) i: low half cos.
-__device__ __forceinline__ void rope_table_entry(const float* __restrict__ freqs,
-                                                 uint32_t* __restrict__ cs, int64_t i, int64_t half,
-                                                 int64_t pos_first, int fixed) {
-  const int64_t t = i / half;
-  const int64_t k = i - t * half;
-  const float p = (float)(fixed ? pos_first : pos_first + t);
-  // frac(p f) in the reference's f32 op order; v_sin_f32 / v_cos_f32 take
-  // their argument in revolutions, so no multiply by 2 pi is needed.  Their
-  // error (~1e-6) is far below the bf16 rounding of the table.
-  const float fr = rope_frac(p, freqs[2 * k]);
-  cs[i] = pack_bf16x2(__builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr));
-}
-
-// The table buffer starts with TABLE_KEY_WORDS int64 words naming the table
-// it holds: magic, T, N/2, first position, fixed flag, frequency pointer
-// (zero on allocation, so a new buffer matches nothing).
-constexpr int TABLE_KEY_WORDS = 8;
-constexpr int64_t TABLE_KEY_MAGIC = 0x62646874626c0001LL;
-
-// V^T and the RoPE table in one launch (both are short and independent):
-// workgroups [0, ntr) are transpose tiles (t fastest, then d, then slab), the
-// rest TBL_PER_WG table entries each (TBL_PER_WG / 256 a thread, so that
-// few workgroups are launched just to find the table already built).
-constexpr int TBL_PER_WG = 4096;
-__global__ __launch_bounds__(256) void prep_bf16_kernel(const bf16_t* __restrict__ v,
-                                                        bf16_t* __restrict__ vt, int64_t T,
-                                                        int64_t D, int64_t Tp, int64_t Dp,
-                                                        int64_t slabs, const float* __restrict__ freqs,
-                                                        uint32_t* __restrict__ cs, int64_t half,
-                                                        int64_t pos_first, int fixed) {
-  const int64_t gt = Tp / VT_TILE, gd = Dp / VT_TILE, ntr = gt * gd * slabs;
-  const int64_t id = blockIdx.x;
-  if (id < ntr) {
-    const int64_t tile = id % (gt * gd);
-    transpose_v_tile(v, vt, T, D, Tp, Dp, id / (gt * gd), (tile % gt) * VT_TILE, (tile / gt) * VT_TILE);
-    return;
-  }
-  // The table depends only on (positions, frequencies): when the key kept in
-  // front of it (written by the previous prefill launch that used it) is
-  // this call's, the entries are already there.
-  const int64_t* key = reinterpret_cast<const int64_t*>(cs) - TABLE_KEY_WORDS;
-  if (key[0] == TABLE_KEY_MAGIC && key[1] == T && key[2] == half && key[3] == pos_first &&
-      key[4] == fixed && key[5] == reinterpret_cast<int64_t>(freqs))
-    return;
-  const int64_t i0 = (id - ntr) * TBL_PER_WG + threadIdx.x;
-#pragma unroll 4
-  for (int j = 0; j < TBL_PER_WG / 256; ++j) {
-    const int64_t i = i0 + j * 256;
-    if (i < T * half) rope_table_entry(freqs, cs, i, half, pos_first, fixed);
-  }
-}
-
 // q[s, t, :] = rope(x[s, t, :]) in bf16: phase frac(p f) in the reference's
 // f32 op order, cos / sin by v_cos_f32 / v_sin_f32 of it, the rotation in f32
 // in the op order of attention.rs:488-501, then rounded to bf16.  Workgroup b
@@ -371,6 +318,12 @@ inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b);
 
 }  // namespace
 
+// Intervals from which a RoPE prefill rotates x in a pass of its own rather
+// than in every launch's tile loads.
+#ifndef BDH_PREROT_MIN_IV
+#define BDH_PREROT_MIN_IV 2
+#endif
+
 bool bf16_shape_supported(int64_t N, int64_t D, const char** why) {
   if (N % T256 != 0) {
     if (why) *why = "bf16 MFMA path needs latent % 256 == 0";
@@ -402,7 +355,6 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   if (a.T * a.N * 2 >= (int64_t)1 << 31 || a.D * (a.T + 64) * 2 >= (int64_t)1 << 31)
     return fail(BDH_UNSUPPORTED, "bf16 MFMA path needs time * latent < 2^30 per stream");
   const int64_t S = a.B * a.H;
-  const int64_t half = a.N / 2;
   // v^T: tokens padded to a multiple of 128 (a state unit's steps cover its
   // interval rounded up to 128 tokens), columns to a multiple of 256 (whole
   // 256-row tiles).
@@ -446,25 +398,19 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     }
   }
 
-  void *vt = nullptr, *part = nullptr, *cs = nullptr, *rdp = nullptr, *rho_a = nullptr, *rho_b = nullptr;
+  void *vt = nullptr, *part = nullptr, *rdp = nullptr, *rho_a = nullptr, *rho_b = nullptr;
   bdh_status stt = scratch(st, SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
   if (stt != BDH_OK) return stt;
   stt = scratch(st, SLOT_SCORES, (size_t)(ks * S * n_iv * Lp * Lp) * sizeof(float), &part);
   if (stt != BDH_OK) return stt;
-  // With two or more intervals every launch would re-read the RoPE table and
-  // re-rotate its x tiles; rotating x once (one read and one write of x)
-  // lets every launch run the table-free units instead.
-  const bool prerot = a.freqs != nullptr && a.state && n_iv >= 2;
+  // With two or more intervals every launch would re-rotate its x tiles;
+  // rotating x once (one read and one write of x) lets every launch run the
+  // rotation-free units instead.
+  const bool prerot = a.freqs != nullptr && a.state && n_iv >= BDH_PREROT_MIN_IV;
   void* xr = nullptr;
   if (prerot) {
     stt = scratch(st, SLOT_ROTATED, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &xr);
     if (stt != BDH_OK) return stt;
-  } else if (a.freqs) {
-    void* tb = nullptr;
-    stt = scratch(st, SLOT_ROPE_TABLE, TABLE_KEY_WORDS * sizeof(int64_t) + (size_t)(a.T * half) * sizeof(uint32_t),
-                  &tb, true);
-    if (stt != BDH_OK) return stt;
-    cs = (char*)tb + TABLE_KEY_WORDS * sizeof(int64_t);
   }
   if (carried) {
     // Two buffers: interval iv's partials go to buffer iv % 2, and their add
@@ -483,15 +429,8 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   const bool rope = a.freqs != nullptr && !prerot;
 
   uint64_t n_launch = 1;
-  if (rope) {
-    const int64_t ntr = (Tp / VT_TILE) * (Dp / VT_TILE) * a.B * a.Hv;
-    hipLaunchKernelGGL(prep_bf16_kernel, dim3((unsigned)ntr + cdiv(a.T * half, TBL_PER_WG)), dim3(256), 0, st,
-                       a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp, a.B * a.Hv, a.freqs, (uint32_t*)cs, half,
-                       a.pos0, a.fixed);
-  } else {
-    hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, VT_TILE), cdiv(Dp, VT_TILE), (unsigned)(a.B * a.Hv)),
-                       dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
-  }
+  hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, VT_TILE), cdiv(Dp, VT_TILE), (unsigned)(a.B * a.Hv)),
+                     dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
   BDH_HIP_TRY(hipGetLastError());
   if (prerot) {
     // Launches of at most 2^22 workgroups (2^30 work-items) each.
@@ -508,14 +447,9 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
 
   PrefillArgs p{};
   p.x = prerot ? (const bf16_t*)xr : a.x;
-  p.cs = (const uint32_t*)cs;
-  if (rope) {
-    // The first prefill launch records which table the buffer now holds.
-    p.table_key = reinterpret_cast<int64_t*>((char*)cs - TABLE_KEY_WORDS * sizeof(int64_t));
-    const int64_t k[6] = {TABLE_KEY_MAGIC, a.T, half, a.pos0, a.fixed,
-                          reinterpret_cast<int64_t>(a.freqs)};
-    for (int i = 0; i < 6; ++i) p.table_key_val[i] = k[i];
-  }
+  p.freqs = rope ? a.freqs : nullptr;
+  p.pos0 = a.pos0;
+  p.fixed = a.fixed;
   p.decay = a.decay;
   p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;
   p.part = (float*)part;
@@ -570,7 +504,6 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     int kt = ktime_begin(BDH_KERNEL_PREFILL, st);
     BDH_HIP_TRY(launch_prefill_mfma(p, rope, st));
     ktime_end(kt, st);
-    p.table_key = nullptr;
     ++n_launch;
     if (a.state && in_place) {
       PrefillArgs q = p;

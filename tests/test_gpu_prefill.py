@@ -134,7 +134,7 @@ def test_bf16_rope_prefill_matches_oracle(oracle, B, H, Hv, T, N, D, with_rho, d
     assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
 
 
-@pytest.mark.parametrize("T", [384, 1100])  # one interval (table path); three (x rotated once)
+@pytest.mark.parametrize("T", [384, 1100])  # one interval (rotated in the tile loads); three (x rotated once)
 def test_bf16_rope_fixed_mode(oracle, T):
     # rotate_positions_fixed (attention.rs:512-550): every token at one position.
     torch = need_gpu()
@@ -171,17 +171,17 @@ def test_bf16_alibi_dense_score_short_context(oracle):
     assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
 
 
-def test_bf16_rope_table_reuse_across_calls(oracle):
-    # The (cos, sin) table is rebuilt only when positions, length or
-    # frequencies change: calls at positions 5, 5, 9, 5 and a longer call
-    # at 5 must each match the oracle.
+def test_bf16_rope_positions_across_calls(oracle):
+    # Each call rotates at its own positions (nothing is kept between calls):
+    # calls at positions 5, 5, 9, 5 and a longer call at 5 must each match
+    # the oracle.
     torch = need_gpu()
     import burn_dragon_amd as bd
     rng = np.random.default_rng(61)
     x, v, _ = _bf16_case(rng, 1, 2, 1, 256, 256, 64, False)
     xl, vl, _ = _bf16_case(rng, 1, 2, 1, 384, 256, 64, False)
     xb, vb, xlb, vlb = (oracle.round_bf16(t) for t in (x, v, xl, vl))
-    announce("bf16 rope table reuse")
+    announce("bf16 rope positions across calls")
     for xx, vv, pos in ((xb, vb, 5), (xb, vb, 5), (xb, vb, 9), (xb, vb, 5), (xlb, vlb, 5)):
         ctx, rho = _run(torch, bd, xx, vv, None, None, dtype=torch.bfloat16, rope=(pos, False))
         cref, rref = oracle.recurrent_f64(oracle.rope_rotate(xx, pos0=pos), vv)

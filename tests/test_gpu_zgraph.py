@@ -1,11 +1,10 @@
 """HIP graph capture of the bf16 prefill.
 
 Scratch is kept per stream: the capture stream is warmed by one eager call,
-then captured.  Between replays run eager calls at other positions (the RoPE
-table, named by a key in device memory, is rebuilt and reused in both
-directions) and at a larger T on the capture stream itself, which grows that
-stream's scratch: the buffers the graph holds are retired, not freed, so
-every replay still equals the eager result."""
+then captured.  Between replays run eager calls at other positions and at a
+larger T on the capture stream itself, which grows that stream's scratch:
+the buffers the graph holds are retired, not freed, so every replay still
+equals the eager result."""
 import pytest
 
 from tests.gpu_util import announce, need_gpu
