@@ -86,7 +86,14 @@ int32_t bdh_supports_backend(void);
  * (in place); otherwise rho_in is not written (the reference's private copy,
  * recurrent.rs:259).  dtype applies to query and value: BDH_F32 runs the
  * fp32 path, BDH_BF16 the MFMA path (fp32 accumulate, fp32 rho/context).
- * chunk: causal block size for the MFMA path (0 = 128).
+ * chunk: the row chunk of the MFMA path, the reference's
+ * dense_score_row_chunk (config.rs:46; linear.rs:117-118): rho is
+ * materialised every `chunk` tokens and the carries inside a row chunk go
+ * through causal score blocks of 128 tokens.  0 = auto: 512 (the
+ * reference's default, config.rs:10), 1024 from time >= 4096; otherwise a
+ * multiple of 128 up to 4096 (BDH_UNSUPPORTED otherwise).  The result does
+ * not depend on it beyond rounding; the fp32 path materialises rho every 256
+ * tokens whatever it is.
  * time == 1 with BDH_F32 (the reference's decode call, sequence_dispatch.rs
  * :109-124; it selects kernels by T, forward_runtime.rs:235-256) runs the
  * one-token step of bdh_decode_step: with rho_out == rho_in and no decay

@@ -188,6 +188,39 @@ def test_bf16_rope_positions_across_calls(oracle):
         assert rel_l2(ctx, cref) <= TOL_BF16 and rel_l2(rho, rref) <= TOL_BF16, pos
 
 
+@pytest.mark.parametrize("chunk", [128, 256, 384, 1024])
+def test_bf16_row_chunk(oracle, chunk):
+    # The row chunk (the reference's dense_score_row_chunk, linear.rs:117-118)
+    # only moves where rho is materialised: T = 1100 with rho in and decay is
+    # 9, 5, 3 or 2 state intervals, each within the bf16 tolerance of the
+    # oracle.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(71 + chunk)
+    x, v, rho0 = _bf16_case(rng, 1, 2, 1, 1100, 256, 64, True)
+    dec = np.array([0.999, 0.998], np.float32)
+    xb, vb = oracle.round_bf16(x), oracle.round_bf16(v)
+    announce("bf16 row chunk", chunk)
+    out = bd.try_fused_recurrent_attention_rope(
+        dev(torch, xb, torch.bfloat16), dev(torch, vb, torch.bfloat16), dev(torch, rho0),
+        dev(torch, dec), position=4, chunk=chunk)
+    torch.cuda.synchronize()
+    assert out is not None
+    cref, rref = oracle.recurrent_f64(oracle.rope_rotate(xb, pos0=4), vb, rho0, dec)
+    assert rel_l2(host(out.context), cref) <= TOL_BF16 and rel_l2(host(out.rho), rref) <= TOL_BF16
+
+
+def test_bf16_row_chunk_outside_the_abi_is_refused():
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    x = torch.zeros(1, 2, 256, 256, device="cuda", dtype=torch.bfloat16)
+    v = torch.zeros(1, 1, 256, 64, device="cuda", dtype=torch.bfloat16)
+    announce("bf16 row chunk refused")
+    for chunk in (-128, 100, 8192):
+        assert bd.try_fused_recurrent_attention_rope(x, v, chunk=chunk) is None, chunk
+    assert bd.try_fused_recurrent_attention_rope(x, v, chunk=4096) is not None
+
+
 def test_bf16_prerotated_query(oracle):
     torch = need_gpu()
     import burn_dragon_amd as bd
