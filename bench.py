@@ -38,11 +38,11 @@ SEED = 20260729
 # profiles/prefill_c2_traffic.txt, profiles/decode_c3_traffic.txt,
 # profiles/long_prefill_c4_traffic.txt.  Counters cannot run inside this
 # process, so the figures are recorded here; they change when the kernels do.
-TRAFFIC_PREFILL_C2 = 1429.6e6       # one prefill_mfma_kernel launch
-TRAFFIC_PREFILL_C2_PASS = 1497.3e6  # the whole C2 pass (prep, prefill, ctx)
+TRAFFIC_PREFILL_C2 = 1027.6e6       # one prefill_mfma_kernel launch
+TRAFFIC_PREFILL_C2_PASS = 1094.9e6  # the whole C2 pass (transpose_v, prefill, ctx)
 TRAFFIC_DECODE_C3 = 428.0e6         # one decode_kernel launch
-TRAFFIC_LONG_C4 = 4475.2e6          # the 16 prefill_mfma_kernel launches of one C4 call
-TRAFFIC_LONG_C4_CALL = 5721.0e6     # the whole C4 call
+TRAFFIC_LONG_C4 = 4322.4e6          # the 8 prefill_mfma_kernel launches of one C4 call (row chunk 1024)
+TRAFFIC_LONG_C4_CALL = 5559.7e6     # the whole C4 call
 
 
 def parse():
