@@ -371,7 +371,14 @@ bdh_status forward_common(const bdh_recurrent_plan* plan, int32_t dtype, const v
     st = scratch(hs, SLOT_SCORES, (size_t)(B * H * Lmax * Lmax) * sizeof(float), &scores);
     if (st != BDH_OK) return st;
     F32Args a{qr, (const float*)v, want_rho ? rho_in : nullptr, decay, ctx, rho_out,
-              (float*)scores, B, H, Hv, T, N, D, Lmax, want_rho};
+              (float*)scores, nullptr, B, H, Hv, T, N, D, Lmax, want_rho};
+    const size_t pe = f32_path_part_elems(a);
+    if (pe) {
+      void* part = nullptr;
+      st = scratch(hs, SLOT_GEMM_PART, pe * sizeof(float), &part);
+      if (st != BDH_OK) return st;
+      a.part = (float*)part;
+    }
     hipError_t e = run_f32_path(a, hs, &prof.launches);
     if (e != hipSuccess) return hip_fail(e, "fp32 path launch");
     prof.done(true);

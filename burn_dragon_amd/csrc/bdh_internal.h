@@ -22,7 +22,7 @@ bdh_status hip_fail(hipError_t e, const char* what);
     if (_e != hipSuccess) return ::bdh::hip_fail(_e, #expr); \
   } while (0)
 
-// Per-device scratch, one buffer per slot, grown on demand (never shrunk).
+// Scratch per (device, stream), one buffer per slot, grown on demand (never shrunk).
 enum ScratchSlot {
   SLOT_SCORES = 0,   // causal score partials    [KS, S, n_iv, Lp, Lp] f32
   SLOT_VT,           // transposed values        [B*Hv, Dp, Tp] bf16
@@ -45,6 +45,7 @@ enum ScratchSlot {
   SLOT_VJP_M,        // VJP GS*D + its transpose     [S, T, T] f32
   SLOT_VJP_TD,       // VJP per-head grad_v, IC, G*d^t  3 x [S, T, D] f32
   SLOT_VJP_PART,     // VJP decay partials           [S] f64
+  SLOT_GEMM_PART,    // fp32 GEMM split-K partials   [P, batch, M, N] f32
   SLOT_COUNT
 };
 // Scratch of the calling stream (see api.hip): grows on first use of a
@@ -85,9 +86,11 @@ struct F32Args {
   float* ctx;           // [S, T, D]
   float* rho_out;       // [S, N, D]
   float* scores;        // scratch [S, Lmax, Lmax]
+  float* part;          // scratch for the GEMMs' split-K partials (f32_path_part_elems floats)
   int64_t B, H, Hv, T, N, D, Lmax;
   bool state;           // false: context only (single interval, no rho)
 };
+size_t f32_path_part_elems(const F32Args& a);
 hipError_t run_f32_path(const F32Args& a, hipStream_t st, uint64_t* launches);
 
 // --- bf16 MFMA path (prefill_bf16.hip) --------------------------------------

@@ -14,92 +14,22 @@
 //            IC = (Q rho0) * d^t                      gemm ROWSCALE + reduction
 //   grad_rho0 = Q^T (G * d^t)               [N, D]   gemm
 // Every product is a batched fp32 GEMM on v_mfma_f32_32x32x2f32 (exact fp32
-// products, fp32 accumulation): 64 x 64 output tiles, 4 waves of 32 x 32,
-// operands staged through LDS 16 deep with generic strides (so transposed
-// operands need no copy).  Reductions are per stream and then per head in a
+// products, fp32 accumulation; bdh_gemm_f32.h) with generic strides, so
+// transposed operands need no copy.  Reductions are per stream and then per head in a
 // fixed order: the result is deterministic.
-#include "bdh_internal.h"
+#include "bdh_gemm_f32.h"
 
 namespace bdh {
 namespace {
 
-enum Epi { E_STORE = 0, E_TRIL, E_TRIL_DECAY, E_ROWSCALE, E_ROWSCALE_ACC };
-
-// C(m, n) = sum_k A(m, k) B(n, k) for batch b = (b / H, b % H):
-//   X(i, j) = X + (b / H) * sXo + (b % H) * sXi + i * sXr + j * sXc.
-struct GemmF32 {
-  const float* A;
-  const float* B;
-  float* C;
-  int64_t sAo, sAi, sAm, sAk;
-  int64_t sBo, sBi, sBn, sBk;
-  int64_t sCo, sCi, sCm, sCn;
-  int M, N, K, H;
-  const float* decay;  // [H] or null (ones): the TRIL_DECAY / ROWSCALE factors
-};
-
-constexpr int GT = 64;
-constexpr int GK = 16;
-
-__device__ __forceinline__ float dpowf(float d, int e) { return powf(d, (float)e); }
-
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
-  __shared__ float As[GK][GT + 4];  // [k][m]
-  __shared__ float Bs[GK][GT + 4];  // [k][n]
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w >> 1, wn = w & 1;
-  const int64_t b = blockIdx.z, bo = b / g.H, bi = b - bo * g.H;
-  const float* A = g.A + bo * g.sAo + bi * g.sAi;
-  const float* B = g.B + bo * g.sBo + bi * g.sBi;
-  float* C = g.C + bo * g.sCo + bi * g.sCi;
-  const int m0 = blockIdx.y * GT, n0 = blockIdx.x * GT;
-  // Loader: 4 elements of each operand per thread and step, consecutive
-  // along whichever index is contiguous in memory.
-  const bool a_kc = g.sAk == 1, b_kc = g.sBk == 1;
-  floatx16 acc = zero16();
-  for (int k0 = 0; k0 < g.K; k0 += GK) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = a_kc ? tid >> 2 : 4 * (tid & 15) + e;
-      const int k = a_kc ? 4 * (tid & 3) + e : tid >> 4;
-      const int gm = m0 + r, gk = k0 + k;
-      As[k][r] = (gm < g.M && gk < g.K) ? A[gm * g.sAm + gk * g.sAk] : 0.0f;
-      const int rn = b_kc ? tid >> 2 : 4 * (tid & 15) + e;
-      const int kn = b_kc ? 4 * (tid & 3) + e : tid >> 4;
-      const int gn = n0 + rn, gkn = k0 + kn;
-      Bs[kn][rn] = (gn < g.N && gkn < g.K) ? B[gn * g.sBn + gkn * g.sBk] : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < GK; kk += 2) {
-      const float a = As[kk + (lane >> 5)][wm * 32 + (lane & 31)];
-      const float bb = Bs[kk + (lane >> 5)][wn * 32 + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc, 0, 0, 0);
-    }
-    __syncthreads();
-  }
-  const float d = g.decay ? g.decay[bi] : 1.0f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int m = m0 + wm * 32 + acc_row(lane, r), n = n0 + wn * 32 + (lane & 31);
-    if (m >= g.M || n >= g.N) continue;
-    float v = acc[r];
-    if (EPI == E_TRIL) v = n < m ? v : 0.0f;
-    if (EPI == E_TRIL_DECAY) v = n < m ? v * dpowf(d, m - n) : 0.0f;
-    if (EPI == E_ROWSCALE || EPI == E_ROWSCALE_ACC) v *= dpowf(d, m);
-    float* dst = C + m * g.sCm + n * g.sCn;
-    if (EPI == E_ROWSCALE_ACC) *dst += v;
-    else *dst = v;
-  }
-}
-
-template <int EPI>
-hipError_t gemm(const GemmF32& g, int64_t batch, hipStream_t st) {
-  const dim3 grid((unsigned)((g.N + GT - 1) / GT), (unsigned)((g.M + GT - 1) / GT), (unsigned)batch);
-  hipLaunchKernelGGL((gemm_f32_kernel<EPI>), grid, dim3(256), 0, st, g);
-  return hipGetLastError();
-}
+using gf32::dpowf;
+using gf32::gemm;
+using gf32::GemmF32;
+using gf32::E_ROWSCALE;
+using gf32::E_ROWSCALE_ACC;
+using gf32::E_STORE;
+using gf32::E_TRIL;
+using gf32::E_TRIL_DECAY;
 
 // M[s, r, c] = W[r, c] + W[c, r], W[r, c] = r > c ? GS[r, c] d^(r - c) : 0.
 __global__ __launch_bounds__(256) void msym_kernel(const float* __restrict__ gs, float* __restrict__ m,
@@ -209,6 +139,19 @@ bdh_status run_attention_vjp(const VjpArgs& a, hipStream_t st, uint64_t* launche
   if (s != BDH_OK) return s;
   s = scratch(st, SLOT_VJP_PART, (size_t)S * sizeof(double), &ppart);
   if (s != BDH_OK) return s;
+  // Split-K partials of the products over N (S and IC) and over T (grad_v).
+  size_t pe = gf32::split_k_elems(S, (int)T, (int)T, (int)N);
+  const size_t pe_ic = gf32::split_k_elems(S, (int)T, (int)D, (int)N);
+  const size_t pe_gv = gf32::split_k_elems(S, (int)T, (int)D, (int)T);
+  pe = pe > pe_ic ? pe : pe_ic;
+  pe = pe > pe_gv ? pe : pe_gv;
+  float* part = nullptr;
+  if (pe) {
+    void* pp = nullptr;
+    s = scratch(st, SLOT_GEMM_PART, pe * sizeof(float), &pp);
+    if (s != BDH_OK) return s;
+    part = (float*)pp;
+  }
   float* Sc = (float*)ps;
   float* GS = (float*)pgs;
   float* Msym = (float*)pm;
@@ -228,15 +171,13 @@ bdh_status run_attention_vjp(const VjpArgs& a, hipStream_t st, uint64_t* launche
   g.B = a.q; g.sBo = H * T * N; g.sBi = T * N; g.sBn = N; g.sBk = 1;
   g.C = Sc; g.sCo = H * TT; g.sCi = TT; g.sCm = T; g.sCn = 1;
   g.M = (int)T; g.N = (int)T; g.K = (int)N;
-  BDH_HIP_TRY(gemm<E_TRIL_DECAY>(g, S, st));
-  ++n;
+  BDH_HIP_TRY(gemm<E_TRIL_DECAY>(g, S, st, part, pe, &n));
   // GS = tril(-1)(G V^T)
   g.A = a.g; g.sAo = H * T * D; g.sAi = T * D; g.sAm = D; g.sAk = 1;
   g.B = a.v; g.sBo = Hv * T * D; g.sBi = sVi; g.sBn = D; g.sBk = 1;
   g.C = GS;
   g.K = (int)D;
-  BDH_HIP_TRY(gemm<E_TRIL>(g, S, st));
-  ++n;
+  BDH_HIP_TRY(gemm<E_TRIL>(g, S, st, part, pe, &n));
   // M = GS * D + (GS * D)^T
   hipLaunchKernelGGL(msym_kernel, dim3(cdivu(TT, 256 * 16) , (unsigned)S), dim3(256), 0, st, (const float*)GS,
                      Msym, a.decay, (int)H, (int)T);
@@ -247,8 +188,7 @@ bdh_status run_attention_vjp(const VjpArgs& a, hipStream_t st, uint64_t* launche
   g.B = a.q; g.sBo = H * T * N; g.sBi = T * N; g.sBn = 1; g.sBk = N;
   g.C = a.grad_q; g.sCo = H * T * N; g.sCi = T * N; g.sCm = N; g.sCn = 1;
   g.M = (int)T; g.N = (int)N; g.K = (int)T;
-  BDH_HIP_TRY(gemm<E_STORE>(g, S, st));
-  ++n;
+  BDH_HIP_TRY(gemm<E_STORE>(g, S, st, part, pe, &n));
   // grad_v = S^T G (per head; summed over heads for shared values)
   g.A = Sc; g.sAo = H * TT; g.sAi = TT; g.sAm = 1; g.sAk = T;
   g.B = a.g; g.sBo = H * T * D; g.sBi = T * D; g.sBn = 1; g.sBk = D;
@@ -259,8 +199,7 @@ bdh_status run_attention_vjp(const VjpArgs& a, hipStream_t st, uint64_t* launche
   }
   g.sCm = D; g.sCn = 1;
   g.M = (int)T; g.N = (int)D; g.K = (int)T;
-  BDH_HIP_TRY(gemm<E_STORE>(g, S, st));
-  ++n;
+  BDH_HIP_TRY(gemm<E_STORE>(g, S, st, part, pe, &n));
   if (Hv == 1) {
     hipLaunchKernelGGL(head_sum_kernel, dim3(cdivu(B * T * D, 256)), dim3(256), 0, st, (const float*)gvh,
                        a.grad_v, B, (int)H, T * D);
@@ -273,15 +212,13 @@ bdh_status run_attention_vjp(const VjpArgs& a, hipStream_t st, uint64_t* launche
     g.B = a.rho0; g.sBo = H * N * D; g.sBi = N * D; g.sBn = 1; g.sBk = D;
     g.C = ic; g.sCo = H * T * D; g.sCi = T * D; g.sCm = D; g.sCn = 1;
     g.M = (int)T; g.N = (int)D; g.K = (int)N;
-    BDH_HIP_TRY(gemm<E_ROWSCALE>(g, S, st));
-    ++n;
+    BDH_HIP_TRY(gemm<E_ROWSCALE>(g, S, st, part, pe, &n));
     // grad_q += (G rho0^T) * d^t
     g.A = a.g; g.sAo = H * T * D; g.sAi = T * D; g.sAm = D; g.sAk = 1;
     g.B = a.rho0; g.sBo = H * N * D; g.sBi = N * D; g.sBn = D; g.sBk = 1;
     g.C = a.grad_q; g.sCo = H * T * N; g.sCi = T * N; g.sCm = N; g.sCn = 1;
     g.M = (int)T; g.N = (int)N; g.K = (int)D;
-    BDH_HIP_TRY(gemm<E_ROWSCALE_ACC>(g, S, st));
-    ++n;
+    BDH_HIP_TRY(gemm<E_ROWSCALE_ACC>(g, S, st, part, pe, &n));
     if (a.grad_rho0) {
       // grad_rho0 = Q^T (G * d^t)
       hipLaunchKernelGGL(rowscale_kernel, dim3(cdivu(S * T * D, 256)), dim3(256), 0, st, a.g, gp, a.decay,
@@ -291,8 +228,8 @@ bdh_status run_attention_vjp(const VjpArgs& a, hipStream_t st, uint64_t* launche
       g.B = gp; g.sBo = H * T * D; g.sBi = T * D; g.sBn = 1; g.sBk = D;
       g.C = a.grad_rho0; g.sCo = H * N * D; g.sCi = N * D; g.sCm = D; g.sCn = 1;
       g.M = (int)N; g.N = (int)D; g.K = (int)T;
-      BDH_HIP_TRY(gemm<E_STORE>(g, S, st));
-      n += 2;
+      BDH_HIP_TRY(gemm<E_STORE>(g, S, st, part, pe, &n));
+      ++n;
     }
   }
   if (a.grad_decay) {
