@@ -50,7 +50,9 @@ struct GemmF32 {
 };
 
 constexpr int GT = 128;   // tile edge
-constexpr int GK = 16;    // k step
+constexpr int GK = 16;               // k step (32 measured slower: 2.24 against 2.17 ms, fp32 C2 shape)
+constexpr int FE = GK / 2;           // operand elements a thread stages per step (128 x GK / 256)
+constexpr int TPK = 256 / GK;        // threads per k row in the row-contiguous loader
 constexpr int GP = 130;   // LDS row pitch (floats): k rows 8 apart fall on different banks
 
 __device__ __forceinline__ float dpowf(float d, int e) { return powf(d, (float)e); }
@@ -59,63 +61,64 @@ __device__ __forceinline__ floatx16 mfma_f32(float a, float b, const floatx16& c
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-// 8 elements of a 128 x 16 operand tile for thread t, rows r0.. of `rows`
-// (R valid), k from kb (K valid):
-//   k-contiguous (sk == 1): row t >> 1, k (t & 1) * 8 .. + 7;
-//   row-contiguous (sr == 1): k t >> 4, rows (t & 15) * 8 .. + 7;
+// FE elements of a 128 x GK operand tile for thread t, rows r0.. (R valid),
+// k from kb (K valid):
+//   k-contiguous (sk == 1): row t >> 1, k (t & 1) * FE .. + FE - 1;
+//   row-contiguous (sr == 1): k t / TPK, rows (t % TPK) * FE .. + FE - 1;
 //   otherwise as k-contiguous, element by element.
 struct Frag {
-  float v[8];
+  float v[FE];
 };
 
 __device__ __forceinline__ void load_frag(const float* X, int64_t sr, int64_t sk, int r0, int R, int kb,
                                           int K, bool vec, int t, Frag& f) {
   if (sr == 1 && sk != 1) {
-    const int k = kb + (t >> 4), r = r0 + (t & 15) * 8;
+    const int k = kb + t / TPK, r = r0 + (t % TPK) * FE;
     const float* p = X + (int64_t)k * sk + r;
-    if (vec && k < K && r + 8 <= R) {
-      const float4 a = *reinterpret_cast<const float4*>(p);
-      const float4 b = *reinterpret_cast<const float4*>(p + 4);
-      f.v[0] = a.x; f.v[1] = a.y; f.v[2] = a.z; f.v[3] = a.w;
-      f.v[4] = b.x; f.v[5] = b.y; f.v[6] = b.z; f.v[7] = b.w;
+    if (vec && k < K && r + FE <= R) {
+#pragma unroll
+      for (int q = 0; q < FE / 4; ++q) {
+        const float4 a = *reinterpret_cast<const float4*>(p + 4 * q);
+        f.v[4 * q] = a.x; f.v[4 * q + 1] = a.y; f.v[4 * q + 2] = a.z; f.v[4 * q + 3] = a.w;
+      }
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f.v[e] = (k < K && r + e < R) ? p[e] : 0.0f;
+      for (int e = 0; e < FE; ++e) f.v[e] = (k < K && r + e < R) ? p[e] : 0.0f;
     }
   } else {
-    const int r = r0 + (t >> 1), k = kb + (t & 1) * 8;
+    const int r = r0 + (t >> 1), k = kb + (t & 1) * FE;
     const float* p = X + (int64_t)r * sr + (int64_t)k * sk;
-    if (vec && sk == 1 && r < R && k + 8 <= K) {
-      const float4 a = *reinterpret_cast<const float4*>(p);
-      const float4 b = *reinterpret_cast<const float4*>(p + 4);
-      f.v[0] = a.x; f.v[1] = a.y; f.v[2] = a.z; f.v[3] = a.w;
-      f.v[4] = b.x; f.v[5] = b.y; f.v[6] = b.z; f.v[7] = b.w;
+    if (vec && sk == 1 && r < R && k + FE <= K) {
+#pragma unroll
+      for (int q = 0; q < FE / 4; ++q) {
+        const float4 a = *reinterpret_cast<const float4*>(p + 4 * q);
+        f.v[4 * q] = a.x; f.v[4 * q + 1] = a.y; f.v[4 * q + 2] = a.z; f.v[4 * q + 3] = a.w;
+      }
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f.v[e] = (r < R && k + e < K) ? p[(int64_t)e * sk] : 0.0f;
+      for (int e = 0; e < FE; ++e) f.v[e] = (r < R && k + e < K) ? p[(int64_t)e * sk] : 0.0f;
     }
   }
 }
 
-// Writes thread t's 8 elements to the [k][row] LDS tile.
+// Writes thread t's FE elements to the [k][row] LDS tile.
 __device__ __forceinline__ void store_frag(float* L, int64_t sr, int64_t sk, int t, const Frag& f) {
   if (sr == 1 && sk != 1) {
-    float* p = L + (t >> 4) * GP + (t & 15) * 8;
+    float* p = L + (t / TPK) * GP + (t % TPK) * FE;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = f.v[e];
+    for (int e = 0; e < FE; ++e) p[e] = f.v[e];
   } else {
-    float* p = L + ((t & 1) * 8) * GP + (t >> 1);
+    float* p = L + ((t & 1) * FE) * GP + (t >> 1);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e * GP] = f.v[e];
+    for (int e = 0; e < FE; ++e) p[e * GP] = f.v[e];
   }
 }
 
 // The k index of element e of thread t's fragment (relative to the step).
 __device__ __forceinline__ int frag_k(int64_t sr, int64_t sk, int t, int e) {
-  return (sr == 1 && sk != 1) ? (t >> 4) : (t & 1) * 8 + e;
+  return (sr == 1 && sk != 1) ? t / TPK : (t & 1) * FE + e;
 }
 
-// The epilogue of element (m, n) of batch b, from its sum v.
 template <int EPI>
 __device__ __forceinline__ void epilogue(const GemmF32& g, int64_t bo, int64_t bi, float d, float carry, int m,
                                          int n, float v) {
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g) {
     if (KSCALE && g.decay) {
       // Padding past K stays 0 (no power of a zero decay with a negative exponent).
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < FE; ++e) {
         const int k = kb + frag_k(g.sAm, g.sAk, t, e);
         if (k < Kt) fa.v[e] *= dpowf(d, g.kpow - k);
       }
@@ -255,11 +258,11 @@ inline bool vec_ok(const float* X, int64_t so, int64_t si, int64_t sr, int64_t s
 }
 
 // Ranges of K to split into: the fewest (a power of two, up to 16) that give
-// the launch two workgroups per CU, each range keeping at least 32 steps.
+// the launch two workgroups per CU, each range keeping at least 512 of K.
 inline int split_k_ranges(int64_t tiles, int K) {
   int p = 1;
   const int64_t want = 2 * (int64_t)device_cus();
-  while (p < 16 && tiles * p < want && K / (2 * p) >= 32 * GK) p *= 2;
+  while (p < 16 && tiles * p < want && K / (2 * p) >= 512) p *= 2;
   return p;
 }
 
