@@ -114,3 +114,36 @@ def test_decode_empty_and_full_rows(oracle):
     assert np.all(host(out.readout)[0, 0] == 0.0)
     assert rel_l2(host(out.readout), a_ref) <= TOL_F32
     assert rel_l2(host(rho_d), rho_ref) <= TOL_F32
+
+
+def test_decode_step_with_pointers_off_16_byte_alignment(oracle):
+    # Tensors that are contiguous views at a 4-byte offset (a storage offset
+    # of one float): the step takes its scalar-column kernel rather than the
+    # float4 one, and matches the oracle; rows outside the active set stay
+    # bit-identical.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    B, H, N, D, pos = 2, 2, 1024, 64, 9
+    rng = np.random.default_rng(4242)
+    x = rc.sparse_relu(rng, (B, H, N))
+    v = rc.gaussian(rng, (B, 1, D), 1 / 16)
+    rho0 = rc.gaussian(rng, (B, H, N, D), 0.5)
+    rho_ref = rho0.copy()
+    a_ref, _, _ = oracle.decode_step_f32(x, v, rho_ref, pos)
+
+    def shifted(a):
+        flat = torch.zeros(a.size + 1, device="cuda")
+        flat[1:] = torch.from_numpy(np.ascontiguousarray(a, np.float32).reshape(-1)).cuda()
+        view = flat[1:].view(a.shape)
+        assert view.data_ptr() % 16 == 4
+        return view
+    xd, vd, rd = shifted(x), shifted(v), shifted(rho0)
+    announce("decode off 16-byte alignment")
+    out = bd.decode_step(xd, vd, rd, position=pos)
+    torch.cuda.synchronize()
+    assert out is not None
+    assert rel_l2(host(out.readout), a_ref) <= TOL_F32
+    assert rel_l2(host(rd), rho_ref) <= TOL_F32
+    partner = x.reshape(B, H, N // 2, 2)[..., ::-1].reshape(B, H, N)
+    untouched = (x == 0) & (partner == 0)
+    assert np.array_equal(host(rd)[untouched], rho0[untouched])
