@@ -12,9 +12,10 @@ closed form (Q = K = query):
   grad_d    = sum(tril(-1)(G V^T) * gap * S) / d  (+ the state term)
   grad_rho0 = (Q * d^t)^T G
 
-The reference computes these in f32; so does this path.  ``None`` is
+The reference computes these in f32; so does this path, at any T (past 1024
+tokens as intervals with a reverse scan of the state gradient).  ``None`` is
 returned where the reference's fused path does not apply (non-f32, not on a
-supported device, T > 4096, mismatched shapes), as the forward ops do.
+supported device, mismatched shapes), as the forward ops do.
 """
 from __future__ import annotations
 
@@ -25,8 +26,6 @@ import torch
 
 from . import _lib
 from .recurrent import CompiledRecurrentAttentionPlan, _ptr, _stream_ptr, supports_backend
-
-MAX_VJP_TIME = 4096
 
 
 class DenseCausalAttentionVjp(NamedTuple):
@@ -58,7 +57,7 @@ def _prep(grad_output, query, value, decay, rho):
     Bv, Hv, Tv, D = value.shape
     if min(B, H, T, N, D) == 0 or Bv != B or Tv != T or Hv not in (1, H):
         return None
-    if tuple(grad_output.shape) != (B, H, T, D) or T > MAX_VJP_TIME:
+    if tuple(grad_output.shape) != (B, H, T, D):
         return None
     if decay is not None and tuple(decay.shape) != (H,):
         return None

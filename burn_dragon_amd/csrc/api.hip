@@ -531,7 +531,6 @@ static bdh_status vjp_common(const bdh_recurrent_plan* plan, const float* query,
                         (const void*)grad_out, (const void*)grad_query, (const void*)grad_value,
                         (const void*)grad_decay, (const void*)grad_rho0})
     if (((uintptr_t)t & 3) != 0) return fail(BDH_EINVAL, "tensor pointers must be 4-byte aligned");
-  if (plan->time > 4096) return fail(BDH_UNSUPPORTED, "the attention VJP needs time <= 4096");
   if (plan->latent > ((int64_t)1 << 24) || plan->embd > ((int64_t)1 << 24))
     return fail(BDH_UNSUPPORTED, "latent and embd must be below 2^24");
   VjpArgs a;

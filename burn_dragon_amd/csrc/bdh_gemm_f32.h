@@ -28,7 +28,8 @@ enum Epi {
   E_TRIL_DECAY,    // C = n < m ? acc * d^(m-n) : 0
   E_ROWSCALE,      // C = acc * d^m
   E_ROWSCALE_ACC,  // C += acc * d^m
-  E_CARRY          // C = acc + src * d^kpow (src null: acc)
+  E_CARRY,         // C = acc + src * d^kpow (src null: acc)
+  E_ROWREV_ACC     // C += acc * d^(kpow - m)
 };
 
 struct GemmF32 {
@@ -126,8 +127,9 @@ __device__ __forceinline__ void epilogue(const GemmF32& g, int64_t bo, int64_t b
   if (EPI == E_TRIL) v = n < m ? v : 0.0f;
   if (EPI == E_TRIL_DECAY) v = n < m ? (g.decay ? v * dpowf(d, m - n) : v) : 0.0f;
   if ((EPI == E_ROWSCALE || EPI == E_ROWSCALE_ACC) && g.decay) v *= dpowf(d, m);
+  if (EPI == E_ROWREV_ACC && g.decay) v *= dpowf(d, g.kpow - m);
   const int64_t o = (int64_t)m * g.sCm + (int64_t)n * g.sCn;
-  if (EPI == E_ROWSCALE_ACC) v += C[o];
+  if (EPI == E_ROWSCALE_ACC || EPI == E_ROWREV_ACC) v += C[o];
   if (EPI == E_CARRY && g.src) v += g.src[bo * g.sCo + bi * g.sCi + o] * carry;
   C[o] = v;
 }

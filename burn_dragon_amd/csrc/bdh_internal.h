@@ -46,6 +46,8 @@ enum ScratchSlot {
   SLOT_VJP_TD,       // VJP per-head grad_v, IC, G*d^t  3 x [S, T, D] f32
   SLOT_VJP_PART,     // VJP decay partials           [S] f64
   SLOT_GEMM_PART,    // fp32 GEMM split-K partials   [P, batch, M, N] f32
+  SLOT_VJP_RHO,      // VJP states at interval starts [n_iv - 1, S, N, D] f32
+  SLOT_VJP_GAMMA,    // VJP state gradients          2 x [S, N, D] f32
   SLOT_COUNT
 };
 // Scratch of the calling stream (see api.hip): grows on first use of a

@@ -176,8 +176,10 @@ bdh_status bdh_dense_causal_attention_fwd(const bdh_recurrent_plan* plan, int32_
  *   Hv = 1), grad_decay [H] (sum((G V^T * gap) * S) / (d + 1e-12) and the
  *   state term), grad_rho0 [B,H,N,D] = (Q * d^t)^T G.
  * decay NULL = ones; rho0 NULL = no state (grad_rho0 must then be NULL);
- * grad_decay and grad_rho0 may be NULL (not computed).  time <= 4096
- * (BDH_UNSUPPORTED beyond); pointers 4-byte aligned. */
+ * grad_decay and grad_rho0 may be NULL (not computed).  Any time: beyond
+ * 1024 tokens the sequence runs as 1024-token intervals with the interval
+ * states recomputed forward and their gradients carried back (scratch of
+ * (time / 1024) x [B,H,N,D] f32).  Pointers 4-byte aligned. */
 bdh_status bdh_dense_causal_attention_vjp(const bdh_recurrent_plan* plan, const float* query,
                                           const float* value, const float* decay, const float* rho0,
                                           const float* grad_output, float* grad_query,

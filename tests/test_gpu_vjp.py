@@ -2,8 +2,10 @@
 (oracle.attention_vjp_f64, pinned by finite differences in
 test_oracle_vjp.py): the reference test's ramp inputs
 (dense_causal_attention/tests.rs:105-183), random shapes with shared and
-per-head values, with and without an initial state, ragged tiles, and the
-recurrent backward's decay defaults.  Bar: rel-L2 <= 1e-5 (fp32)."""
+per-head values, with and without an initial state, ragged tiles, sequences
+longer than one 1024-token interval (the reverse scan of the state
+gradient), and the recurrent backward's decay defaults.  Bar: rel-L2 <= 1e-5
+(fp32)."""
 import numpy as np
 import pytest
 
@@ -45,6 +47,9 @@ def test_vjp_reference_ramps(oracle):
     (1, 2, 2, 70, 96, 40, False, [0.95, 0.9]),                # ragged tiles, per-head values
     (2, 2, 1, 300, 256, 96, True, [0.999, 0.99]),
     (1, 4, 1, 512, 1024, 256, False, None),                   # decay ones
+    (1, 2, 1, 1100, 64, 32, True, [0.999, 0.998]),            # 2 intervals (1024 + 76): reverse scan
+    (1, 2, 2, 2100, 64, 24, False, [0.9995, 0.999]),          # 3 intervals, per-head values
+    (2, 1, 1, 2048, 128, 64, True, None),                     # 2 whole intervals, decay ones
 ])
 def test_vjp_matches_oracle(oracle, B, H, Hv, T, N, D, with_rho, decay):
     torch = need_gpu()
@@ -100,7 +105,32 @@ def test_vjp_none_cases():
     assert bd.dense_causal_attention_vjp(g, q, v, d) is not None
     assert bd.dense_causal_attention_vjp(g.bfloat16(), q.bfloat16(), v.bfloat16(), d) is None
     assert bd.dense_causal_attention_vjp(g, q, torch.zeros(1, 3, 8, 4, device="cuda"), d) is None
+    assert bd.dense_causal_attention_vjp(g, q, v, torch.ones(3, device="cuda")) is None
+    # Any length is served (five intervals here); zero inputs give zero gradients.
     big = torch.zeros(1, 1, 4097, 8, device="cuda")
-    assert bd.dense_causal_attention_vjp(torch.zeros(1, 1, 4097, 4, device="cuda"), big,
-                                         torch.zeros(1, 1, 4097, 4, device="cuda"),
-                                         torch.ones(1, device="cuda")) is None
+    out = bd.dense_causal_attention_vjp(torch.zeros(1, 1, 4097, 4, device="cuda"), big,
+                                        torch.zeros(1, 1, 4097, 4, device="cuda"), torch.ones(1, device="cuda"))
+    torch.cuda.synchronize()
+    assert out is not None
+    assert not out.grad_query.any() and not out.grad_value.any() and not out.grad_decay.any()
+
+
+def test_recurrent_vjp_over_several_intervals(oracle):
+    # The recurrent backward past one interval: the incoming rho's gradient
+    # comes back through three interval states.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(7901)
+    B, H, T, N, D = 1, 2, 2500, 64, 32
+    q = rc.gaussian(rng, (B, H, T, N), 0.1)
+    v = rc.gaussian(rng, (B, 1, T, D))
+    g = rc.gaussian(rng, (B, H, T, D))
+    rho = rc.gaussian(rng, (B, H, N, D), 0.1)
+    dec = np.array([0.9993, 0.9985], np.float32)
+    announce("recurrent vjp intervals", T)
+    out = bd.recurrent_attention_vjp(dev(torch, g), dev(torch, q), dev(torch, v), dev(torch, rho),
+                                     dev(torch, dec))
+    torch.cuda.synchronize()
+    assert out is not None
+    gq, gv, gd, gr = oracle.attention_vjp_f64(q, v, g, dec, rho, safe="recurrent")
+    _cmp((out.grad_query, out.grad_value, out.grad_decay, out.grad_rho), (gq, gv, gd, gr))
