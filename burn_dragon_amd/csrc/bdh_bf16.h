@@ -152,7 +152,7 @@ struct PrefillArgs {
   int gram_groups;      // S * ks * n_iv
   int gram_ids;         // workgroup ids reserved for gram units (prefill_gram_ids)
   // state units
-  const bf16_t* vt;     // [B*Hv, Dp, Tp], zero past (D, T); Dp = D rounded up to 256
+  const bf16_t* vt;     // v^T [B*Hv, Tp/32, Dp, 32] (step-major), zero past (D, T); Dp = D rounded up to 256
   const float* rho_in;  // [S, N, D] or null
   float* rho_out;       // [S, N, D]
   int64_t st_t0, st_Lc, Tp, Dp;  // Tp >= st_t0 + st_Lc rounded up to 64
@@ -172,7 +172,33 @@ struct PrefillArgs {
   float* add_ctx;       // [S, T, D]
   int64_t add_t0, add_Lc;
   int add_units;
+  // readout units of every interval iv >= rd_iv0 at once (rd_snap set; x
+  // pre-rotated, no decay): rd_part [rd_kr, S, T, D] = q rho_iv over the
+  // kr-th N range, rho_iv from rd_snap [n_iv, S, D, N] bf16 (prefill_carry_kernel)
+  const bf16_t* rd_snap;
+  int64_t rd_iv0;
 };
+
+// --- launch interface of the state-carry kernel (carry_prefill.hip) --------
+// One workgroup per (stream, 128-neuron block, 256-column block) walks every
+// token of the call with its block of rho in registers (no decay):
+// rho_{iv+1} = rho_iv + Q_iv^T V_iv.  It writes snap[iv] = rho_iv as bf16
+// [d][n] for every interval with a carried state (iv >= 1, and iv = 0 when
+// rho_in is set), the final rho in f32, and, when it rotates, q = RoPE(x).
+struct CarryArgs {
+  const bf16_t* x;      // [S, T, N]
+  const float* freqs;   // RoPE frequencies [N], or null (x already rotated; q unused)
+  int64_t pos0;
+  int fixed;
+  int64_t H, Hv, T, N, D, S, L, Tp, Dp;  // L a multiple of 128; Tp = T rounded up to 128
+  const bf16_t* vt;     // v^T [B*Hv, Tp/32, Dp, 32] (step-major), zero past (D, T)
+  const float* rho_in;  // [S, N, D] or null
+  float* rho_out;       // [S, N, D] (may be rho_in)
+  bf16_t* snap;         // [n_iv, S, D, N]
+  bf16_t* q;            // [S, T, N] rotated queries (freqs set)
+};
+int prefill_carry_units(int64_t S, int64_t N, int64_t Dp);
+hipError_t launch_prefill_carry(const CarryArgs& a, hipStream_t st);
 
 // RoPE position of token t of the call (attention.rs:488-501 with the
 // Sequential or Fixed positions of the call): exact in f32 below 2^24.

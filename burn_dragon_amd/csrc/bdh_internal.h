@@ -25,7 +25,7 @@ bdh_status hip_fail(hipError_t e, const char* what);
 // Scratch per (device, stream), one buffer per slot, grown on demand (never shrunk).
 enum ScratchSlot {
   SLOT_SCORES = 0,   // causal score partials    [KS, S, n_iv, Lp, Lp] f32
-  SLOT_VT,           // transposed values        [B*Hv, Dp, Tp] bf16
+  SLOT_VT,           // transposed values        [B*Hv, Tp/32, Dp, 32] bf16
   SLOT_ROTATED,      // rotated queries [S, T, N]: f32 (fp32 path) or bf16 (bf16 path)
   SLOT_READOUT,      // readout partials (bf16 path) [rd_kr, S, Lp, D] f32
   SLOT_RHO_A,        // states between intervals (bf16 path) [S, N, D] f32
@@ -48,6 +48,7 @@ enum ScratchSlot {
   SLOT_GEMM_PART,    // fp32 GEMM split-K partials   [P, batch, M, N] f32
   SLOT_VJP_RHO,      // VJP states at interval starts [n_iv - 1, S, N, D] f32
   SLOT_VJP_GAMMA,    // VJP state gradients          2 x [S, N, D] f32
+  SLOT_SNAP,         // states at interval starts (bf16 path) [n_iv, S, D, N] bf16
   SLOT_COUNT
 };
 // Scratch of the calling stream (see api.hip): grows on first use of a

@@ -232,10 +232,11 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
   const int tp = tid & 15, nv = tid >> 4;
   const uint32_t xlane = (uint32_t)(2 * tp * rowb + (n0 + 8 * nv) * 2);
   // v^T loader: 4 lanes per 64-byte segment of a row d, rows vb + 64 i (v^T
-  // has Dp = D rounded up to 256 rows, zero past D).
+  // has Dp = D rounded up to 256 rows, zero past D; a step's rows are
+  // contiguous).
   const int kc = tid & 3, vb = tid >> 2;
-  const int64_t vrow = a.Tp * 2;
-  const uint32_t vlane = (uint32_t)(vb * vrow + kc * 16);
+  const int64_t vstep = a.Dp * 64;  // bytes of one 32-token step of v^T
+  const uint32_t vlane = (uint32_t)(vb * 64 + kc * 16);
   // Uniform base and per-lane offset of token tb + i's 16 bytes for this
   // lane in the [token][N] x.
   auto at = [&](int kt, int i, uint32_t& off) -> int64_t {
@@ -267,7 +268,7 @@ __device__ __forceinline__ void state_unit(const PrefillArgs& a, bf16_t* lds, in
     }
     const int64_t tb = t0 + (int64_t)kt * BK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st.vr[i] = ldg16_off(VT + (d0 + 64 * i) * vrow + tb * 2, vlane);
+    for (int i = 0; i < 4; ++i) st.vr[i] = ldg16_off(VT + (tb >> 5) * vstep + (d0 + 64 * i) * 64, vlane);
   };
   auto store = [&](int buf) {
     bf16_t* A = lds + buf * BUF;             // [n][t], 128 rows
@@ -422,6 +423,79 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
 }
 
 // ---------------------------------------------------------------------------
+// readout unit over a bf16 state snapshot: rd_part[kp, s, t0 + r, d] =
+// sum over the kp-th N range of q[s, t0 + r, n] rho_iv[n, d] for rows
+// r0 .. r0+255 of interval iv (t0 = iv L) and columns d0 .. d0+127.  Both
+// operands are k-contiguous bf16 rows (q rows; rho_iv^T rows of snap[iv]),
+// so they are fetched straight into a three-stage LDS ring two steps ahead,
+// as the rotation-free gram tiles do.  Stage rows: q rows 0..255, then
+// rho^T rows 256..383.  Rows past a ragged interval re-read its last row,
+// columns past D re-read column D - 1; neither is stored.
+template <bool WHOLE>
+__device__ __forceinline__ void readout_snap_unit(const PrefillArgs& a, bf16_t* lds, int64_t s, int kp,
+                                                  int64_t iv, int64_t r0, int64_t d0) {
+  const int lane = threadIdx.x & 63, w = wave_id();
+  const int64_t t0 = iv * a.L;
+  const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
+  const int64_t rowb = a.N * 2;  // bytes per q row and per rho^T row
+  const char* X = reinterpret_cast<const char*>(a.x + (s * a.T + t0) * a.N);
+  const char* R = reinterpret_cast<const char*>(a.rd_snap + (iv * a.S + s) * a.D * a.N);
+  const int nk = (int)(a.N / BK);
+  const int kb = (int)((int64_t)nk * kp / a.rd_kr), ke = (int)((int64_t)nk * (kp + 1) / a.rd_kr);
+  constexpr int groups = 6;
+  const uint32_t gc = (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
+  uint32_t voff[groups];
+  int64_t vbase[groups];
+#pragma unroll
+  for (int j = 0; j < groups; ++j) {
+    // Wave w fetches rows 16 w .. 16 w + 15 of group j (stage block w + 4 j).
+    if (j < 4) {
+      const int64_t rr = r0 + 64 * j + 16 * w;
+      if (WHOLE) {
+        vbase[j] = rr * rowb;
+        voff[j] = (uint32_t)((lane >> 2) * rowb) + gc * 16;
+      } else {
+        const int64_t t = rr + (lane >> 2);
+        vbase[j] = 0;
+        voff[j] = (uint32_t)((t < Lc ? t : Lc - 1) * rowb) + gc * 16;
+      }
+    } else {
+      const int64_t d = d0 + 64 * (j - 4) + 16 * w + (lane >> 2);
+      vbase[j] = 0;
+      voff[j] = (uint32_t)((d < a.D ? d : a.D - 1) * rowb) + gc * 16;
+    }
+  }
+  constexpr int STAGE = groups * 64 * BK;  // bf16 elements of one stage
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  auto issue = [&](int kt, int stg) {
+    const int64_t kofs = (int64_t)kt * 64;
+#pragma unroll
+    for (int j = 0; j < groups; ++j)
+      dma16((j < 4 ? X : R) + vbase[j] + kofs, voff[j], lds0 + (uint32_t)(stg * STAGE * 2 + (w + 4 * j) * 1024));
+  };
+  floatx4 acc[4][8];
+  zero_acc(acc);
+  const bool active = r0 + 64 * w < Lc;
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): see the gram ring
+  issue(kb, 0);
+  issue(kb + 1 < ke ? kb + 1 : kb, 1);
+  int stg = 0;
+  for (int kt = kb; kt < ke; ++kt) {
+    dma_wait_barrier<groups>();
+    issue(kt + 2 < ke ? kt + 2 : ke - 1, stg == 0 ? 2 : stg - 1);
+    if (active) mma_64x128_dsasm(lds + stg * STAGE, lds + stg * STAGE, lane, 64 * w, T256, acc);
+    stg = stg == 2 ? 0 : stg + 1;
+  }
+  dma_wait_barrier<0>();  // the epilogue reuses the ring
+  float* P = a.rd_part + ((int64_t)kp * a.S + s) * a.T * a.D + t0 * a.D;
+  epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
+    const int64_t t = r0 + 64 * w + row, d = d0 + col;
+    if (t < Lc && d < a.D)
+      __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, reinterpret_cast<floatx4*>(&P[t * a.D + d]));
+  });
+}
+
+// ---------------------------------------------------------------------------
 // add unit aid: a contiguous share of the previous interval's (s, t, float4)
 // context elements; the partials are summed in split order onto ctx (the
 // order of readout_add_kernel).
@@ -529,6 +603,24 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
     const int ndb = (int)((a.D + T256 / 2 - 1) / (T256 / 2));
     const int64_t d0 = (int64_t)(rid % ndb) * (T256 / 2);
     rid /= ndb;
+    if constexpr (!ROPE && !DECAY) {
+      if (a.rd_snap) {
+        // (stream, interval >= rd_iv0, 256-row block): interval fastest after
+        // the row block, so a group of ids spans the intervals of a stream.
+        const int nrb = (int)(a.Lp / T256);
+        const int64_t r0 = (int64_t)(rid % nrb) * T256;
+        rid /= nrb;
+        const int64_t niv = a.n_iv - a.rd_iv0;
+        const int64_t iv = a.rd_iv0 + rid % niv;
+        const int64_t s = rid / niv;
+        const int64_t t0 = iv * a.L;
+        const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
+        if (r0 >= Lc) return;  // past a ragged last interval
+        if (r0 + T256 <= Lc) readout_snap_unit<true>(a, lds, s, kp, iv, r0, d0);
+        else readout_snap_unit<false>(a, lds, s, kp, iv, r0, d0);
+        return;
+      }
+    }
     const int nrb = (int)((a.rd_Lc + T256 - 1) / T256);
     const int64_t r0 = (int64_t)(rid % nrb) * T256;
     const int64_t s = rid / nrb;

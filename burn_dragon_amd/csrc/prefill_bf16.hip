@@ -37,12 +37,17 @@ __device__ __forceinline__ int cofs(int r, int c) { return r * CK + ((c ^ ((r >>
 // launch writes for all intervals.  (The readout of a carried state is added
 // per interval by readout_add_kernel.)
 struct CtxArgs {
-  const bf16_t* vt;      // [B*Hv, Dp, Tp]
+  const bf16_t* vt;      // v^T [B*Hv, Tp/32, Dp, 32]
   const float* part;     // gram partials [KS, S, n_iv, Lp, Lp]
   float* ctx;            // [S, T, D]
   int64_t H, Hv, T, D, L, Lp, Tp, Dp, S, n_iv;
   int iv0, n_ivc;        // intervals covered by this launch
   int nrb;               // CTX_ROWS row blocks per interval: ceil(min(L, T) / 64)
+  // Readout partials added to the context of intervals iv >= rd_iv0 (null:
+  // none): rd [rd_kr, S, T, D], summed in split order.
+  const float* rd;
+  int rd_kr;
+  int64_t rd_iv0;
 };
 
 // Workgroup id -> (row block, interval, stream): row blocks heaviest first
@@ -69,7 +74,7 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int64_t b = s / a.H, h = s - b * a.H;
-  const bf16_t* VT = a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp + t0;
+  const bf16_t* VT = a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp + (t0 >> 5) * (a.Dp * 32);
   const int64_t pstride = a.S * a.n_iv * a.Lp * a.Lp;
   const float* P0 = a.part + (s * a.n_iv + iv) * a.Lp * a.Lp;
   const int64_t ecol = e0 + wave * WC;  // this wave's WC output columns
@@ -80,8 +85,9 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
   const int nk = (int)((kend + CK - 1) / CK);
 
   // Loaders.  Scores: 8 lanes per 32-column row segment (4 floats each),
-  // rows m and m + 32.  v^T: 4 lanes per 64-byte row segment, rows dv + 64 i
-  // (v^T is zero past D up to Dp, a multiple of 256, so no column test).
+  // rows m and m + 32.  v^T: 4 lanes per 64-byte row segment of the step,
+  // rows dv + 64 i (v^T is zero past D up to Dp, a multiple of 256, so no
+  // column test).
   const int sm = tid >> 3, sc = tid & 7;
   const int dv = tid >> 2, kc = tid & 3;
   struct Stage {
@@ -100,7 +106,7 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
-    for (int i = 0; i < NI * 2; ++i) st.v[i] = ldg16(VT + (e0 + dv + 64 * i) * a.Tp + k0 + kc * 8);
+    for (int i = 0; i < NI * 2; ++i) st.v[i] = ldg16(VT + (k0 >> 5) * (a.Dp * 32) + (e0 + dv + 64 * i) * 32 + kc * 8);
   };
   auto store = [&](int kt) {
     const int64_t k0 = (int64_t)kt * CK;
@@ -167,6 +173,9 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
 
   if (!wave_on) return;
   float* C = a.ctx + (s * a.T + t0) * a.D;
+  const bool rd = a.rd != nullptr && iv >= a.rd_iv0;
+  const float* RD = rd ? a.rd + (s * a.T + t0) * a.D : nullptr;
+  const int64_t rd_stride = a.S * a.T * a.D;
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -175,7 +184,12 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int64_t row = r0 + mi * 32 + acc_row(lane, r);
         const int64_t d = ecol + ni * 32 + acc_col(lane);
-        if (row < Lc && d < a.D) C[row * a.D + d] = acc[mi][ni][r];
+        if (row < Lc && d < a.D) {
+          float v = acc[mi][ni][r];
+          if (rd)
+            for (int kp = 0; kp < a.rd_kr; ++kp) v += RD[kp * rd_stride + row * a.D + d];
+          C[row * a.D + d] = v;
+        }
       }
 }
 
@@ -223,12 +237,15 @@ __global__ __launch_bounds__(256) void readout_add_kernel(const float* __restric
   *reinterpret_cast<float4*>(&ctx[(s * T + t0 + t) * D + d]) = v;
 }
 
-// vt[bv, d, t] = v[bv, t, d] for t < T, d < D; 0 for T <= t < Tp or D <= d < Dp:
-// the 32 x 32 tile (t0, d0) of slab bv.
-// One 64 x 64 tile of v^T (tokens t0 .., columns d0 ..): 16-byte loads of v
+// v^T, step-major: element (bv, d, t) at bv Dp Tp + (t / 32) Dp 32 + d 32 +
+// t % 32, = v[bv, t, d] for t < T, d < D and 0 for T <= t < Tp or D <= d < Dp.
+// One 32-token step of every column is then one contiguous Dp x 64-byte
+// block, so a consumer's 64-byte row segments of a step come in 1 KiB runs
+// per wave load (with rows of Tp tokens they were 64-byte pieces 2 Tp bytes
+// apart).  One 64 x 64 tile (tokens t0 .., columns d0 ..): 16-byte loads of v
 // rows (8 columns; D is a multiple of 32, so 8 columns are all inside D or
-// all past it) into LDS, 16-byte stores of v^T rows (8 tokens; Tp is a
-// multiple of 128).  Zeros past T and D.
+// all past it) into LDS, 16-byte stores of 8 tokens (Tp is a multiple of
+// 128).  Zeros past T and D.
 constexpr int VT_TILE = 64;
 __device__ __forceinline__ void transpose_v_tile(const bf16_t* __restrict__ v, bf16_t* __restrict__ vt,
                                                  int64_t T, int64_t D, int64_t Tp, int64_t Dp,
@@ -257,7 +274,8 @@ __device__ __forceinline__ void transpose_v_tile(const bf16_t* __restrict__ v, b
       // element r of tokens c + 2j and c + 2j + 1: the low or high half of their words
       w[j] = (r & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
     }
-    *reinterpret_cast<uint4*>(vt + (bv * Dp + d) * Tp + t) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(vt + bv * Dp * Tp + (t >> 5) * (Dp * 32) + d * 32 + (t & 31)) =
+        make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
@@ -349,6 +367,103 @@ int device_cus() {
   return cached[dev];
 }
 
+// Largest bf16 state-snapshot buffer of the state-carry form; past it the
+// per-interval launch chain runs (two f32 states).
+constexpr size_t kCarrySnapMax = (size_t)8 << 30;
+
+namespace {
+// Two or more intervals, no decay: v^T, the state-carry kernel (which also
+// rotates x once and writes q), one launch of every interval's gram tiles
+// and readouts (from the bf16 snapshots), then the context kernel, which
+// adds the readout partials.  Four launches whatever the interval count.
+bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, int64_t S, int64_t Tp,
+                          int64_t Dp, int64_t n_iv, int64_t Lp, int nb, int nk) {
+  const bool rope = a.freqs != nullptr;
+  const int64_t L = a.L;
+  const int64_t rd_iv0 = a.rho_in ? 0 : 1;
+  const int ndb = (int)cdiv(a.D, T256 / 2);
+  // Split counts as in the interval chain: the fewest N splits for which the
+  // longest unit stays within ~85% of the average work per workgroup slot
+  // (work in 32-deep steps of one 256 x 128 tile).
+  const double gram_work = (double)S * n_iv * nb * (nb + 1) * nk;
+  const double rd_work = (double)S * (n_iv - rd_iv0) * nb * ndb * nk;
+  const double per_slot = (gram_work + rd_work) / (2.0 * device_cus());
+  int ks = 1, kr = 1;
+  for (int cand = 1; cand <= 8 && nk % (2 * cand) == 0; cand *= 2) {
+    ks = cand;
+    if ((double)nk / cand <= 0.85 * per_slot) break;
+  }
+  for (int cand = 1; cand <= 16 && nk % (2 * cand) == 0; cand *= 2) {
+    kr = cand;
+    if ((double)nk / cand <= 0.85 * per_slot) break;
+  }
+
+  void *vt = nullptr, *part = nullptr, *snap = nullptr, *rdp = nullptr, *q = nullptr;
+  bdh_status stt = scratch(st, SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
+  if (stt != BDH_OK) return stt;
+  stt = scratch(st, SLOT_SCORES, (size_t)(ks * S * n_iv * Lp * Lp) * sizeof(float), &part);
+  if (stt != BDH_OK) return stt;
+  stt = scratch(st, SLOT_SNAP, (size_t)(n_iv * S * a.D * a.N) * sizeof(bf16_t), &snap);
+  if (stt != BDH_OK) return stt;
+  stt = scratch(st, SLOT_READOUT, (size_t)(kr * S * a.T * a.D) * sizeof(float), &rdp);
+  if (stt != BDH_OK) return stt;
+  if (rope) {
+    stt = scratch(st, SLOT_ROTATED, (size_t)(S * a.T * a.N) * sizeof(bf16_t), &q);
+    if (stt != BDH_OK) return stt;
+  }
+
+  hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, VT_TILE), cdiv(Dp, VT_TILE), (unsigned)(a.B * a.Hv)),
+                     dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
+  BDH_HIP_TRY(hipGetLastError());
+
+  CarryArgs c{};
+  c.x = a.x;
+  c.freqs = a.freqs;
+  c.pos0 = a.pos0;
+  c.fixed = a.fixed;
+  c.H = a.H; c.Hv = a.Hv; c.T = a.T; c.N = a.N; c.D = a.D; c.S = S; c.L = L; c.Tp = Tp; c.Dp = Dp;
+  c.vt = (const bf16_t*)vt;
+  c.rho_in = a.rho_in;
+  c.rho_out = a.rho_out;
+  c.snap = (bf16_t*)snap;
+  c.q = (bf16_t*)q;
+  int kt = ktime_begin(BDH_KERNEL_PREFILL, st);
+  BDH_HIP_TRY(launch_prefill_carry(c, st));
+  ktime_end(kt, st);
+
+  PrefillArgs p{};
+  p.x = rope ? (const bf16_t*)q : a.x;
+  p.freqs = nullptr;
+  p.pos0 = a.pos0;
+  p.fixed = a.fixed;
+  p.decay = nullptr;
+  p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;
+  p.part = (float*)part;
+  p.L = L; p.Lp = Lp; p.n_iv = n_iv;
+  p.ks = ks; p.nb = nb;
+  p.gram_groups = (int)(S * ks * n_iv);
+  p.gram_ids = prefill_gram_ids(p.gram_groups, nb);
+  p.vt = (const bf16_t*)vt;
+  p.Tp = Tp; p.Dp = Dp;
+  p.state_units = 0;
+  p.rd_part = (float*)rdp;
+  p.rd_kr = kr;
+  p.rd_units = (int)(S * (n_iv - rd_iv0) * nb * ndb * kr);
+  p.rd_snap = (const bf16_t*)snap;
+  p.rd_iv0 = rd_iv0;
+  p.add_units = 0;
+  kt = ktime_begin(BDH_KERNEL_PREFILL, st);
+  BDH_HIP_TRY(launch_prefill_mfma(p, false, st));
+  ktime_end(kt, st);
+
+  CtxArgs cx{(const bf16_t*)vt, (const float*)part, a.ctx, a.H, a.Hv, a.T, a.D, L, Lp, Tp, Dp, S,
+             n_iv, 0, (int)n_iv, (int)cdiv(L, CTX_ROWS), (const float*)rdp, kr, rd_iv0};
+  BDH_HIP_TRY(launch_ctx(cx, ks, st));
+  if (launches) *launches += 4;
+  return BDH_OK;
+}
+}  // namespace
+
 bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) {
   // The MFMA kernels address one stream's x, its RoPE table rows and one
   // v^T slab with 32-bit byte offsets.
@@ -367,6 +482,10 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   const int nb = (int)(Lp / T256);
   const int nk = (int)(a.N / 32);  // 32-deep gram steps
   const int state_units = prefill_state_units(S, a.N, a.D);
+  // (The readout units address a snapshot's rows with 32-bit offsets.)
+  if (a.state && n_iv >= 2 && a.decay == nullptr && a.D * a.N * 2 < ((int64_t)1 << 31) &&
+      (size_t)(n_iv * S * a.N * a.D) * sizeof(bf16_t) <= kCarrySnapMax)
+    return run_carry_path(a, st, launches, S, Tp, Dp, n_iv, Lp, nb, nk);
 
   // N splits of the gram: the fewest for which the longest gram unit stays
   // within ~85% of the first launch's average work per workgroup slot (two
@@ -520,7 +639,7 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
       // tril(S) V of every interval: the gram partials are all written by
       // the first launch.
       CtxArgs c{(const bf16_t*)vt, (const float*)part, a.ctx, a.H, a.Hv, a.T, a.D, L, Lp, Tp, Dp, S,
-                n_iv, 0, (int)(a.state ? n_iv : 1), (int)cdiv(Lc0, CTX_ROWS)};
+                n_iv, 0, (int)(a.state ? n_iv : 1), (int)cdiv(Lc0, CTX_ROWS), nullptr, 0, 0};
       BDH_HIP_TRY(launch_ctx(c, ks, st));
       ++n_launch;
     }

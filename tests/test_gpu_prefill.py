@@ -301,3 +301,43 @@ def test_bf16_decay_zero_and_negative(oracle, decay):
     assert np.isfinite(ctx).all() and np.isfinite(rho).all()
     assert rel_l2(ctx, cref) <= TOL_BF16
     assert rel_l2(rho, rref) <= TOL_BF16
+
+
+@pytest.mark.parametrize("B,H,Hv,T,N,D,with_rho,chunk,rope,inplace", [
+    (1, 2, 1, 1100, 256, 64, True, 128, (4, False), False),    # 9 intervals, ragged last
+    (1, 2, 2, 1100, 512, 320, False, 256, (9, False), False),  # two column blocks, per-head V, no rho
+    (2, 2, 1, 1024, 256, 96, True, 384, (1000, True), False),  # L not a multiple of 256, fixed positions
+    (1, 2, 1, 700, 256, 64, True, 256, None, False),           # pre-rotated query
+    (1, 2, 1, 1100, 256, 64, True, 512, (3, False), True),     # rho updated in place
+])
+def test_bf16_state_carry_path(oracle, B, H, Hv, T, N, D, with_rho, chunk, rope, inplace):
+    # Two or more intervals without decay run the state-carry kernel (every
+    # rho block carried across the intervals in registers, bf16 snapshots at
+    # the interval starts) and one launch of every interval's gram tiles and
+    # readouts.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(T + N + D + chunk)
+    x, v, rho0 = _bf16_case(rng, B, H, Hv, T, N, D, with_rho)
+    xb, vb = oracle.round_bf16(x), oracle.round_bf16(v)
+    if rope is None:
+        xb = oracle.round_bf16(oracle.rope_rotate(xb, pos0=0))
+        q = xb
+    else:
+        q = oracle.rope_rotate(xb, pos0=rope[0], mode=1 if rope[1] else 0)
+    announce("bf16 state carry", B, H, Hv, T, N, D, with_rho, chunk, rope, inplace)
+    xd, vd = dev(torch, xb, torch.bfloat16), dev(torch, vb, torch.bfloat16)
+    rd = dev(torch, rho0) if with_rho else None
+    if rope is None:
+        out = bd.try_fused_recurrent_attention(xd, vd, rd, None, inplace=inplace, chunk=chunk)
+    else:
+        out = bd.try_fused_recurrent_attention_rope(xd, vd, rd, None, position=rope[0], fixed=rope[1],
+                                                    inplace=inplace, chunk=chunk)
+    torch.cuda.synchronize()
+    assert out is not None
+    if inplace:
+        assert out.rho.data_ptr() == rd.data_ptr()
+    cref, rref = oracle.recurrent_f64(q, vb, rho0)
+    e_ctx, e_rho = rel_l2(host(out.context), cref), rel_l2(host(out.rho), rref)
+    print(f"rel-L2 ctx {e_ctx:.2e} rho {e_rho:.2e}")
+    assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
