@@ -38,11 +38,11 @@ SEED = 20260729
 # profiles/prefill_c2_traffic.txt, profiles/decode_c3_traffic.txt,
 # profiles/long_prefill_c4_traffic.txt.  Counters cannot run inside this
 # process, so the figures are recorded here; they change when the kernels do.
-TRAFFIC_PREFILL_C2 = 1027.6e6       # one prefill_mfma_kernel launch
-TRAFFIC_PREFILL_C2_PASS = 1094.9e6  # the whole C2 pass (transpose_v, prefill, ctx)
+TRAFFIC_PREFILL_C2 = 1049.5e6       # one prefill_mfma_kernel launch
+TRAFFIC_PREFILL_C2_PASS = 1116.8e6  # the whole C2 pass (transpose_v, prefill, ctx)
 TRAFFIC_DECODE_C3 = 428.0e6         # one decode_kernel launch
-TRAFFIC_LONG_C4 = 4322.4e6          # the 8 prefill_mfma_kernel launches of one C4 call (row chunk 1024)
-TRAFFIC_LONG_C4_CALL = 5559.7e6     # the whole C4 call
+TRAFFIC_LONG_C4 = 3567.0e6          # the carry and prefill_mfma launches of one C4 call (row chunk 512)
+TRAFFIC_LONG_C4_CALL = 3695.3e6     # the whole C4 call
 
 
 def parse():
@@ -199,8 +199,9 @@ def bench_prefill(torch, args):
 
 
 def bench_long(torch, args):
-    """C4: one long stream per head, T = 8192 (8 state-carry intervals at the
-    automatic row chunk)."""
+    """C4: one long stream per head, T = 8192 (16 state-carry intervals at the
+    automatic row chunk of 512: the state-carry launch, then one launch of every
+    interval's gram and readout tiles)."""
     from burn_dragon_amd import _lib
     B, H, T, N, D, C = 1, 4, 8192, 8192, 256, 256
     dev = torch.device("cuda")
@@ -225,8 +226,8 @@ def bench_long(torch, args):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     # The same call at the config's row chunk of 256 (32 state intervals):
-    # the result is the same up to rounding; the automatic row chunk (1024
-    # at this length) is the faster schedule.
+    # the result is the same up to rounding; the automatic row chunk (512)
+    # writes half the state snapshots.
     for _ in range(2):
         lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho, chunk=C)
     e0.record()
@@ -237,26 +238,29 @@ def bench_long(torch, args):
     ms_c = e0.elapsed_time(e1) / steps
     flop = B * H * T * (4 * N * D + (C - 1) * (N + D))
     call_tflops = flop / (ms * 1e-3) / 1e12
-    # The dominant kernel: its launches per call (one per state interval), summed.
+    # The dominant kernels: a call's state-carry launch and its gram/readout
+    # launch, summed (they hold all of the call's algorithmic work but the
+    # intra-chunk S.V term).
     k_ms, k_n = timed_kernel(torch, lib, _lib.BDH_KERNEL_PREFILL, steps,
                              lambda: lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho))
     k_flop = B * H * T * (4 * N * D + (C - 1) * N)
     achieved = k_flop / (k_ms * 1e-3) / 1e12
     print(f"[long] {ms:.3f} ms/prefill, {B * T / (ms * 1e-3) / 1e6:.2f} M tok/s, "
-          f"{call_tflops:.1f} TFLOP/s per call; prefill_mfma_kernel {k_n:.0f} launches, "
+          f"{call_tflops:.1f} TFLOP/s per call; carry + prefill_mfma kernels {k_n:.0f} launches, "
           f"{k_ms:.3f} ms, {achieved:.1f} TFLOP/s; at row chunk {C}: {ms_c:.3f} ms", flush=True)
     return {"metric": "C4 long-context prefill tokens/s per BDH layer", "value": B * T / (ms * 1e-3),
             "unit": "tokens/s", "ms_per_prefill": ms, "steps": steps,
             "config": {"workload": "C4 long prefill, one BDH layer: B1 nh4 T8192 N8192 D256, "
                                    "bf16 in / fp32 acc, RoPE fused; automatic row chunk (rho "
-                                   "materialised every 1024 tokens), credited at the config's "
+                                   "snapshots every 512 tokens), credited at the config's "
                                    f"chunk {C}"},
             "at_config_chunk": {"chunk": C, "ms_per_prefill": round(ms_c, 4),
                                 "tokens_per_s": round(B * T / (ms_c * 1e-3), 1)},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                          "traffic": TRAFFIC_LONG_C4,
-                         "kernel": f"prefill_mfma_kernel, {k_n:.0f} launches per call (summed)",
+                         "kernel": f"prefill_carry_kernel + prefill_mfma_kernel, {k_n:.0f} launches "
+                                   "per call (summed)",
                          "kernel_ms_per_call": round(k_ms, 4), "flop_per_call": k_flop,
                          "call": {"tflops": round(call_tflops, 2), "flop": flop, "traffic": TRAFFIC_LONG_C4_CALL}}}
 

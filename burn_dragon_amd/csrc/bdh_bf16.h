@@ -150,7 +150,7 @@ struct PrefillArgs {
   int64_t L, Lp, n_iv;
   int ks, nb;           // N splits (N/32 a multiple of 4 ks); 256-row blocks per interval
   int gram_groups;      // S * ks * n_iv
-  int gram_ids;         // workgroup ids reserved for gram units (prefill_gram_ids)
+  int gram_ids;         // workgroup ids of the gram groups (prefill_gram_ids), readout tiles included
   // state units
   const bf16_t* vt;     // v^T [B*Hv, Tp/32, Dp, 32] (step-major), zero past (D, T); Dp = D rounded up to 256
   const float* rho_in;  // [S, N, D] or null
@@ -172,11 +172,13 @@ struct PrefillArgs {
   float* add_ctx;       // [S, T, D]
   int64_t add_t0, add_Lc;
   int add_units;
-  // readout units of every interval iv >= rd_iv0 at once (rd_snap set; x
-  // pre-rotated, no decay): rd_part [rd_kr, S, T, D] = q rho_iv over the
-  // kr-th N range, rho_iv from rd_snap [n_iv, S, D, N] bf16 (prefill_carry_kernel)
+  // snapshot mode (rd_snap set; x pre-rotated, no decay): rd_pg readout
+  // tiles per gram group, for every interval iv >= rd_iv0, over the group's
+  // N range (rd_kr = ks): rd_part [rd_kr, S, T, D] = q rho_iv, rho_iv from
+  // rd_snap [n_iv, S, D, N] bf16 (prefill_carry_kernel)
   const bf16_t* rd_snap;
   int64_t rd_iv0;
+  int rd_pg;
 };
 
 // --- launch interface of the state-carry kernel (carry_prefill.hip) --------
@@ -230,7 +232,7 @@ __device__ __forceinline__ uint4 rope_cs4(float p, const float (&f)[4]) {
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
 // Workgroup ids a gram launch needs for `groups` groups of nb-block
 // intervals (ids are laid out so that one group's tiles share an XCD).
-int prefill_gram_ids(int groups, int nb);
+int prefill_gram_ids(int groups, int nb, int rd_pg = 0);
 // State units of one interval.
 int prefill_state_units(int64_t S, int64_t N, int64_t D);
 // Readout units of one interval of Lc rows.

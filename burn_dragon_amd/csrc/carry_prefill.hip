@@ -27,54 +27,82 @@ namespace {
 using namespace mfma;
 
 constexpr int CARRY_N = T256 / 2;  // neurons per block
-constexpr int CARRY_P = 4;         // steps of loads in flight
+constexpr int CARRY_R = 5;         // ring stages: loads run CARRY_R - 2 steps ahead
+// LDS bytes: ring stages of raw x [32 tokens][128 neurons] (8 KiB) + v^T
+// [256 columns][32 tokens] (16 KiB), then the double-buffered q^T [128][32].
+constexpr int CARRY_STAGE = 24 * 1024;
+constexpr int CARRY_XT = CARRY_R * CARRY_STAGE;
+constexpr int CARRY_LDS = CARRY_XT + 2 * 8 * 1024;
+// Vector memory operations a wave issues per step: 2 x DMAs + 4 v^T DMAs,
+// plus its 2 q stores when it writes q.  Waiting for at most 18 in flight at
+// the start of step k leaves stage k landed: in steady state 2 + 2 x 8 (or
+// 2 x 6) operations follow stage k's DMAs; in the first steps (stages issued
+// by the prologue, 6 each) at least 18.  With q stores the wait also covers
+// one step more than needed (the ring then runs 2 steps ahead, not 3).
+constexpr int CARRY_WAIT = 18;
 
 template <bool ROPE, bool QOUT>
-__device__ __forceinline__ void carry_unit(const CarryArgs& a, bf16_t* lds, int64_t s, int64_t n0,
+__device__ __forceinline__ void carry_unit(const CarryArgs& a, char* lds, int64_t s, int64_t n0,
                                            int64_t d0) {
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int wm = w >> 1, wn = w & 1;  // n rows 64 wm .., d columns 128 wn ..
   const int64_t b = s / a.H, h = s - b * a.H;
   const int64_t rowb = a.N * 2;  // bytes per x row
   const char* X = reinterpret_cast<const char*>(a.x + s * a.T * a.N);
-  const char* VT = reinterpret_cast<const char*>(a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp);
+  const char* VT = reinterpret_cast<const char*>(a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp) + d0 * 64;
   bf16_t* Q = QOUT ? a.q + s * a.T * a.N : nullptr;
-
-  // x loader: tokens 2 tp, 2 tp + 1 of the step x neurons n0 + 8 nv .. + 7;
-  // tokens past T re-read row T - 1 (their v^T columns are zero).
-  const int tp = tid & 15, nv = tid >> 4;
-  const uint32_t xcol = (uint32_t)((n0 + 8 * nv) * 2);
-  // v^T loader: 4 lanes per 64-byte segment of a row d, rows vb + 64 i (a
-  // step's rows are contiguous).
-  const int kc = tid & 3, vb = tid >> 2;
   const int64_t vstep = a.Dp * 64;  // bytes of one 32-token step of v^T
-  const uint32_t vlane = (uint32_t)(vb * 64 + kc * 16);
-  float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (ROPE) load_freq4(a.freqs + n0 + 8 * nv, fq);
+  const int nk = (int)(a.Tp / BK);  // a multiple of 4 (Tp: T rounded up to 128)
+  const int spi = (int)(a.L / BK);  // steps per interval
 
-  struct Stage {
-    uint4 xr[2], vr[4];
-  };
-  auto load = [&](Stage& st, int kt) {
-    const int64_t tb = (int64_t)kt * BK;
+  // DMA lanes.  x: 1 KiB blocks of 4 rows x 256 bytes (128 neurons); wave w
+  // fetches blocks w and w + 4; LDS chunk c of row r holds global chunk
+  // c ^ (r & 15), so that the readers below (16 rows, one chunk column) hit
+  // distinct banks.  v^T: 1 KiB blocks of 16 rows x 64 bytes, blocks w + 4 j;
+  // the lane writing slot c of row r fetches chunk c ^ ((r >> 1) & 3), the
+  // swizzle of the MFMA operand layout (lds_off).
+  int xrow[2];
+  uint32_t xcol[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int64_t t = tb + 2 * tp + i;
-      st.xr[i] = ldg16_off(X, (uint32_t)((t < a.T ? t : a.T - 1) * rowb) + xcol);
+  for (int j = 0; j < 2; ++j) {
+    xrow[j] = 4 * (w + 4 * j) + (lane >> 4);
+    xcol[j] = (uint32_t)((n0 + 8 * ((lane & 15) ^ (xrow[j] & 15))) * 2);
+  }
+  uint32_t voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 16 * (w + 4 * j) + (lane >> 2);
+    voff[j] = (uint32_t)(r * 64 + (((lane & 3) ^ ((r >> 1) & 3)) * 16));
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  auto issue = [&](int kt, int slot) {
+    const int64_t tb = (int64_t)kt * BK;
+    const uint32_t base = lds0 + (uint32_t)(slot * CARRY_STAGE);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t t = tb + xrow[j];
+      dma16(X, (uint32_t)((t < a.T ? t : a.T - 1) * rowb) + xcol[j], base + (uint32_t)((w + 4 * j) * 1024));
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st.vr[i] = ldg16_off(VT + (int64_t)kt * vstep + (d0 + 64 * i) * 64, vlane);
+    for (int j = 0; j < 4; ++j)
+      dma16(VT + (int64_t)kt * vstep, voff[j], base + 8192u + (uint32_t)((w + 4 * j) * 1024));
   };
-  auto store = [&](const Stage& st, int kt, int buf) {
-    bf16_t* A = lds + buf * BUF;             // q^T [n][t], 128 rows
-    bf16_t* B = lds + buf * BUF + 128 * BK;  // v^T [d][t], 256 rows
-    // Tokens past T hold row T - 1 (see load) and are rotated at its
-    // position, so their q is row T - 1's and is stored there again (the
-    // same bytes): every step issues the same memory operations, and the
-    // compiler's waits for a stage loaded CARRY_P steps ago stay exact.
+
+  // Rotation lanes: tokens 2 tp, 2 tp + 1 of the step x neurons n0 + 8 nv ..
+  const int tp = tid & 15, nv = tid >> 4;
+  float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (ROPE) load_freq4(a.freqs + n0 + 8 * nv, fq);
+  // q^T of step k (tokens 2 tp, 2 tp + 1 of neuron 8 nv + e) into buffer k & 1.
+  auto rotate = [&](int kt, int slot) {
+    const char* R = lds + slot * CARRY_STAGE;
+    const int r0 = 2 * tp, r1 = 2 * tp + 1;
+    uint4 q0 = *reinterpret_cast<const uint4*>(R + r0 * 256 + ((nv ^ (r0 & 15)) << 4));
+    uint4 q1 = *reinterpret_cast<const uint4*>(R + r1 * 256 + ((nv ^ (r1 & 15)) << 4));
+    // Tokens past T hold row T - 1 (see issue) and are rotated at its
+    // position, so their q is row T - 1's and is stored there again (the same
+    // bytes); their v^T columns are zero, so they add nothing to rho.
     const int64_t t = (int64_t)kt * BK + 2 * tp;
     const int64_t ta = t < a.T ? t : a.T - 1, tb = t + 1 < a.T ? t + 1 : a.T - 1;
-    uint4 q0 = st.xr[0], q1 = st.xr[1];
     if (ROPE) {
       // Sums of integers below 2^24 are exact in f32.
       const float pa = (float)(a.fixed ? a.pos0 : a.pos0 + ta);
@@ -91,14 +119,12 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, bf16_t* lds, int6
     }
     // q^T: word (neuron e, tokens 2 tp, 2 tp + 1) from the two tokens' words.
     const uint32_t u0[4] = {q0.x, q0.y, q0.z, q0.w}, u1[4] = {q1.x, q1.y, q1.z, q1.w};
-    uint32_t* Aw = reinterpret_cast<uint32_t*>(A);
+    uint32_t* Aw = reinterpret_cast<uint32_t*>(lds + CARRY_XT + (kt & 1) * 8192);
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       Aw[(lds_off(8 * nv + 2 * p, tp >> 2) + 2 * (tp & 3)) >> 1] = (u0[p] & 0xffffu) | (u1[p] << 16);
       Aw[(lds_off(8 * nv + 2 * p + 1, tp >> 2) + 2 * (tp & 3)) >> 1] = (u0[p] >> 16) | (u1[p] & 0xffff0000u);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&B[lds_off(vb + 64 * i, kc)]) = st.vr[i];
   };
 
   const bool active = d0 + 128 * wn < a.D;
@@ -108,7 +134,7 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, bf16_t* lds, int6
   const int64_t nl = n0 + 64 * wm + 4 * (lane >> 4);
   const int64_t dl = d0 + 128 * wn + (lane & 15);
   if (a.rho_in && active) {
-    const float* R = a.rho_in + s * a.N * a.D;
+    const float* Rin = a.rho_in + s * a.N * a.D;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -116,7 +142,7 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, bf16_t* lds, int6
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int64_t d = dl + 16 * ni;
-          acc[mi][ni][r] = d < a.D ? R[(nl + 16 * mi + r) * a.D + d] : 0.0f;
+          acc[mi][ni][r] = d < a.D ? Rin[(nl + 16 * mi + r) * a.D + d] : 0.0f;
         }
   } else {
     zero_acc(acc);
@@ -137,32 +163,34 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, bf16_t* lds, int6
                          pack_bf16x2(acc[mi][ni][2], acc[mi][ni][3]));
       }
   };
-
-  const int nk = (int)(a.Tp / BK);  // a multiple of 4 (Tp: T rounded up to 128)
-  const int spi = (int)(a.L / BK);  // steps per interval, a multiple of 4
-  Stage st[CARRY_P];
-#pragma unroll
-  for (int j = 0; j < CARRY_P; ++j) load(st[j], j);  // nk >= 4
   if (a.rho_in) snapshot(0);
-  for (int kt = 0; kt < nk; kt += CARRY_P) {
-#pragma unroll
-    for (int j = 0; j < CARRY_P; ++j) {
-      const int k = kt + j;
-      store(st[j], k, k & 1);
-      // Also orders this buffer's writes after every wave's MFMA reads of
-      // step k - 2 (which finished before the previous step's barrier).
-      __syncthreads();
-      // Past the end the last step is loaded again (unused): no branch, so
-      // the wait for each stage covers only its own loads.
-      load(st[j], k + CARRY_P < nk ? k + CARRY_P : nk - 1);
-      if (active) mma_64x128(lds + (k & 1) * BUF, lds + (k & 1) * BUF + 128 * BK, lane, 64 * wm, 128 * wn, acc);
-    }
-    // Interval boundaries fall on multiples of spi steps (CARRY_P divides spi).
-    if ((kt + CARRY_P) % spi == 0 && kt + CARRY_P < nk) snapshot((kt + CARRY_P) / spi);
-  }
-  __syncthreads();  // the epilogue reuses the LDS buffers
 
-  epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
+  // Every load above has completed before the ring starts (the compiler cannot
+  // see the DMAs, so it must not be left waiting for older loads inside it).
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+#pragma unroll
+  for (int j = 0; j < CARRY_R - 1; ++j) issue(j, j);  // nk >= 4 = CARRY_R - 1
+  int slot = 0;  // ring slot of step k
+  for (int k = 0; k < nk; ++k) {
+    // Stage k has landed for every wave, and every wave has finished the LDS
+    // reads of step k - 1 (slot k - 1 and the q^T buffer of step k - 1 are free).
+    dma_wait_barrier<CARRY_WAIT>();
+    // Step k + CARRY_R - 1 into slot k - 1; past the end the last step is
+    // fetched again (unused), so every step issues the same operations.
+    const int nxt = k + CARRY_R - 1 < nk ? k + CARRY_R - 1 : nk - 1;
+    issue(nxt, slot == 0 ? CARRY_R - 1 : slot - 1);
+    rotate(k, slot);
+    __syncthreads();  // q^T of step k written
+    if (active)
+      mma_64x128_dsasm(reinterpret_cast<const bf16_t*>(lds + CARRY_XT + (k & 1) * 8192),
+                       reinterpret_cast<const bf16_t*>(lds + slot * CARRY_STAGE + 8192), lane, 64 * wm,
+                       128 * wn, acc);
+    slot = slot == CARRY_R - 1 ? 0 : slot + 1;
+    if ((k + 1) % spi == 0 && k + 1 < nk) snapshot((k + 1) / spi);
+  }
+  dma_wait_barrier<0>();  // the epilogue reuses the ring
+
+  epilogue_64x128(acc, reinterpret_cast<bf16_t*>(lds), w, lane, [&](int row, int col, float4 v) {
     const int64_t n = n0 + 64 * wm + row, d = d0 + 128 * wn + col;
     if (d >= a.D) return;
     __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w},
@@ -172,7 +200,7 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, bf16_t* lds, int6
 
 template <bool ROPE>
 __global__ __launch_bounds__(NT, 1) void prefill_carry_kernel(CarryArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * BUF];
+  __shared__ __attribute__((aligned(16))) char lds[CARRY_LDS];
   const int nt = (int)(a.N / CARRY_N);
   const int dt = (int)(a.Dp / T256);
   const int units = (int)(a.S * nt * dt);

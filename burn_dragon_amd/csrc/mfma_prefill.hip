@@ -559,9 +559,9 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[3 * BUF];
   const int id = blockIdx.x;
   if (id < a.gram_ids) {
-    const int tpg = units_per_group(a.nb);
+    const int tpg = units_per_group(a.nb) + a.rd_pg;
     const int blk = id / (8 * tpg), rem = id - blk * 8 * tpg;
-    const int u = rem >> 3;
+    int u = rem >> 3;
     const int g = blk * 8 + (rem & 7);
     if (g >= a.gram_groups) return;
     const int64_t iv = g % a.n_iv;
@@ -570,6 +570,21 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
     const int64_t s = q / a.ks;
     const int64_t t0 = iv * a.L;
     const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
+    if (u < a.rd_pg) {
+      // Readout tiles of the group's interval and N range (snapshot mode):
+      // they read the same q rows as the group's gram tiles, at the same time
+      // and on the same XCD, so those rows come from L2 rather than HBM.
+      if constexpr (!ROPE && !DECAY) {
+        if (iv < a.rd_iv0) return;
+        const int ndb = (int)((a.D + T256 / 2 - 1) / (T256 / 2));
+        const int64_t r0 = (int64_t)(u / ndb) * T256, d0 = (int64_t)(u % ndb) * (T256 / 2);
+        if (r0 >= Lc) return;  // past a ragged last interval
+        if (r0 + T256 <= Lc) readout_snap_unit<true>(a, lds, s, kp, iv, r0, d0);
+        else readout_snap_unit<false>(a, lds, s, kp, iv, r0, d0);
+      }
+      return;
+    }
+    u -= a.rd_pg;
     if (u >= a.nb * a.nb) {
       // Pair of diagonal blocks of row blocks 2j and 2j + 1.
       const int j = u - a.nb * a.nb;
@@ -603,24 +618,6 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
     const int ndb = (int)((a.D + T256 / 2 - 1) / (T256 / 2));
     const int64_t d0 = (int64_t)(rid % ndb) * (T256 / 2);
     rid /= ndb;
-    if constexpr (!ROPE && !DECAY) {
-      if (a.rd_snap) {
-        // (stream, interval >= rd_iv0, 256-row block): interval fastest after
-        // the row block, so a group of ids spans the intervals of a stream.
-        const int nrb = (int)(a.Lp / T256);
-        const int64_t r0 = (int64_t)(rid % nrb) * T256;
-        rid /= nrb;
-        const int64_t niv = a.n_iv - a.rd_iv0;
-        const int64_t iv = a.rd_iv0 + rid % niv;
-        const int64_t s = rid / niv;
-        const int64_t t0 = iv * a.L;
-        const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
-        if (r0 >= Lc) return;  // past a ragged last interval
-        if (r0 + T256 <= Lc) readout_snap_unit<true>(a, lds, s, kp, iv, r0, d0);
-        else readout_snap_unit<false>(a, lds, s, kp, iv, r0, d0);
-        return;
-      }
-    }
     const int nrb = (int)((a.rd_Lc + T256 - 1) / T256);
     const int64_t r0 = (int64_t)(rid % nrb) * T256;
     const int64_t s = rid / nrb;
@@ -646,8 +643,8 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
 
 }  // namespace
 
-int prefill_gram_ids(int groups, int nb) {
-  const int tpg = nb * nb + (nb + 1) / 2;
+int prefill_gram_ids(int groups, int nb, int rd_pg) {
+  const int tpg = nb * nb + (nb + 1) / 2 + rd_pg;
   return ((groups + 7) / 8) * 8 * tpg;
 }
 

@@ -382,21 +382,20 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   const int64_t L = a.L;
   const int64_t rd_iv0 = a.rho_in ? 0 : 1;
   const int ndb = (int)cdiv(a.D, T256 / 2);
-  // Split counts as in the interval chain: the fewest N splits for which the
-  // longest unit stays within ~85% of the average work per workgroup slot
-  // (work in 32-deep steps of one 256 x 128 tile).
+  // The readout tiles of an interval join its gram group (same N range, same
+  // XCD, dispatched together): they read the same q rows.  N splits as in the
+  // interval chain: the fewest for which the longest unit stays within ~85%
+  // of the average work per workgroup slot (work in 32-deep steps of one
+  // 256 x 128 tile).
   const double gram_work = (double)S * n_iv * nb * (nb + 1) * nk;
   const double rd_work = (double)S * (n_iv - rd_iv0) * nb * ndb * nk;
   const double per_slot = (gram_work + rd_work) / (2.0 * device_cus());
-  int ks = 1, kr = 1;
+  int ks = 1;
   for (int cand = 1; cand <= 8 && nk % (2 * cand) == 0; cand *= 2) {
     ks = cand;
     if ((double)nk / cand <= 0.85 * per_slot) break;
   }
-  for (int cand = 1; cand <= 16 && nk % (2 * cand) == 0; cand *= 2) {
-    kr = cand;
-    if ((double)nk / cand <= 0.85 * per_slot) break;
-  }
+  const int kr = ks;
 
   void *vt = nullptr, *part = nullptr, *snap = nullptr, *rdp = nullptr, *q = nullptr;
   bdh_status stt = scratch(st, SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
@@ -442,13 +441,14 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   p.L = L; p.Lp = Lp; p.n_iv = n_iv;
   p.ks = ks; p.nb = nb;
   p.gram_groups = (int)(S * ks * n_iv);
-  p.gram_ids = prefill_gram_ids(p.gram_groups, nb);
+  p.rd_pg = nb * ndb;
+  p.gram_ids = prefill_gram_ids(p.gram_groups, nb, p.rd_pg);
   p.vt = (const bf16_t*)vt;
   p.Tp = Tp; p.Dp = Dp;
   p.state_units = 0;
   p.rd_part = (float*)rdp;
   p.rd_kr = kr;
-  p.rd_units = (int)(S * (n_iv - rd_iv0) * nb * ndb * kr);
+  p.rd_units = 0;
   p.rd_snap = (const bf16_t*)snap;
   p.rd_iv0 = rd_iv0;
   p.add_units = 0;
