@@ -383,18 +383,16 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   const int64_t rd_iv0 = a.rho_in ? 0 : 1;
   const int ndb = (int)cdiv(a.D, T256 / 2);
   // The readout tiles of an interval join its gram group (same N range, same
-  // XCD, dispatched together): they read the same q rows.  N splits as in the
-  // interval chain: the fewest for which the longest unit stays within ~85%
-  // of the average work per workgroup slot (work in 32-deep steps of one
-  // 256 x 128 tile).
-  const double gram_work = (double)S * n_iv * nb * (nb + 1) * nk;
-  const double rd_work = (double)S * (n_iv - rd_iv0) * nb * ndb * nk;
-  const double per_slot = (gram_work + rd_work) / (2.0 * device_cus());
-  int ks = 1;
-  for (int cand = 1; cand <= 8 && nk % (2 * cand) == 0; cand *= 2) {
-    ks = cand;
-    if ((double)nk / cand <= 0.85 * per_slot) break;
-  }
+  // XCD, dispatched together): they read the same q rows.  N splits: 1 or 2,
+  // whichever gives the fewer steps in rounds of units over the workgroup
+  // slots (two per CU), 1 on a tie (every split writes, and the context
+  // kernel re-reads, one more set of partials).  Measured at C4, chunk 512:
+  // 576 units of 256 steps take 2 rounds, 1152 of 128 steps 3 (0.85 against
+  // 0.875 ms per call); 4 splits were slower at every chunk.
+  const int64_t slots = 2 * (int64_t)device_cus();
+  const int64_t upg = (int64_t)nb * nb + (nb + 1) / 2 + (int64_t)nb * ndb;
+  auto rounds = [&](int k) { return (S * n_iv * k * upg + slots - 1) / slots * (nk / k); };
+  const int ks = (nk % 4 == 0 && rounds(2) < rounds(1)) ? 2 : 1;
   const int kr = ks;
 
   void *vt = nullptr, *part = nullptr, *snap = nullptr, *rdp = nullptr, *q = nullptr;
