@@ -22,10 +22,14 @@ namespace bdh {
 // Every op rounds separately: contraction is off in these bodies (an FMA
 // would subtract floor() from the unrounded product).  The active-row test
 // frac != 0 must agree bit for bit with the reference's f32 arithmetic.
+// raw - floor(raw) is exact for finite raw >= 0 (positions and frequencies
+// are never negative), so v_fract_f32, which computes it in one instruction
+// (and clamps below 1.0 only where the difference would round to 1.0), gives
+// the same bits as the reference's two operations.
 __device__ __forceinline__ float rope_frac(float p, float f) {
 #pragma clang fp contract(off)
   const float raw = p * f;
-  return raw - floorf(raw);
+  return __builtin_amdgcn_fractf(raw);
 }
 __device__ __forceinline__ float rope_phase(float p, float f) {
 #pragma clang fp contract(off)
