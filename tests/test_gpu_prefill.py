@@ -341,3 +341,32 @@ def test_bf16_state_carry_path(oracle, B, H, Hv, T, N, D, with_rho, chunk, rope,
     e_ctx, e_rho = rel_l2(host(out.context), cref), rel_l2(host(out.rho), rref)
     print(f"rel-L2 ctx {e_ctx:.2e} rho {e_rho:.2e}")
     assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
+
+
+@pytest.mark.parametrize("B,H,Hv,T,N,D,decay,rope", [
+    (1, 2, 1, 300, 256, 96, None, (17, False)),                 # ragged T inside one 512-token interval
+    (1, 2, 2, 700, 512, 320, None, (5, False)),                 # three 256-row blocks, two column blocks
+    (2, 2, 1, 512, 256, 64, [0.97, 0.95], (0, False)),          # decay (gram and state weights)
+    (1, 2, 1, 1024, 256, 64, None, (2000, True)),               # four row blocks, fixed positions
+])
+def test_bf16_one_interval_cases(oracle, B, H, Hv, T, N, D, decay, rope):
+    # One interval (row chunk 1024) with RoPE in the tile loads and no carried
+    # state: ragged lengths, several 256-row blocks and column blocks, decay,
+    # fixed positions.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(T + N + 3 * D)
+    x, v, _ = _bf16_case(rng, B, H, Hv, T, N, D, False)
+    xb, vb = oracle.round_bf16(x), oracle.round_bf16(v)
+    dec = np.array(decay, np.float32) if decay else None
+    announce("bf16 one interval", B, H, Hv, T, N, D, decay, rope)
+    out = bd.try_fused_recurrent_attention_rope(
+        dev(torch, xb, torch.bfloat16), dev(torch, vb, torch.bfloat16), None,
+        dev(torch, dec) if dec is not None else None, position=rope[0], fixed=rope[1], chunk=1024)
+    torch.cuda.synchronize()
+    assert out is not None
+    q = oracle.rope_rotate(xb, pos0=rope[0], mode=1 if rope[1] else 0)
+    cref, rref = oracle.recurrent_f64(q, vb, None, dec)
+    e_ctx, e_rho = rel_l2(host(out.context), cref), rel_l2(host(out.rho), rref)
+    print(f"rel-L2 ctx {e_ctx:.2e} rho {e_rho:.2e}")
+    assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
