@@ -144,8 +144,20 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // bytes).  Written in assembly so that the compiler, which does not know
 // which LDS bytes a DMA writes, does not wait for every DMA in flight before
 // each LDS read; the pipeline's own waits (dma_wait_barrier) order them.
+// gbase is wave-uniform at every call; it is read from the first lane so
+// that it is an SGPR pair even where the compiler kept it in VGPRs.  The
+// builtin returns a signed int: each half goes through uint32_t, or the low
+// half would be sign-extended into the high one.  The compiler does not see
+// the load inside the assembly, so the block waits 5 states itself (an SGPR
+// written by a VALU instruction, such as v_readfirstlane, needs 5 before a
+// vector memory instruction reads it; M0 needs 1 before an LDS DMA).
 __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t m0) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(gbase), "{m0}"(m0)
+  const uint64_t b = reinterpret_cast<uint64_t>(gbase);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t bu = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(reinterpret_cast<const void*>(bu)),
+               "{m0}"(m0)
                : "memory");
 }
 // Wait until at most N of this wave's vector memory operations are in
