@@ -63,7 +63,7 @@ def parse():
                          "of the FETCH_SIZE / WRITE_SIZE counter runs); 'rmw' measures the HBM "
                          "ceilings (read, copy, in-place RMW, RMW of random 1 KiB rows) on a "
                          "buffer the size of C3's rho")
-    ap.add_argument("--long-steps", type=int, default=3, help="timed C4 prefills")
+    ap.add_argument("--long-steps", type=int, default=10, help="timed C4 prefills")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="target CPU-baseline wall time (split between prefill and decode)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -199,9 +199,9 @@ def bench_prefill(torch, args):
 
 
 def bench_long(torch, args):
-    """C4: one long stream per head, T = 8192 (16 state-carry intervals at the
-    automatic row chunk of 512: the state-carry launch, then one launch of every
-    interval's gram and readout tiles)."""
+    """C4: one long stream per head, T = 8192 (8 state-carry intervals at the
+    automatic row chunk of 1024: the state-carry launch, then one launch of
+    every interval's gram and readout tiles)."""
     from burn_dragon_amd import _lib
     B, H, T, N, D, C = 1, 4, 8192, 8192, 256, 256
     dev = torch.device("cuda")
@@ -226,8 +226,8 @@ def bench_long(torch, args):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     # The same call at the config's row chunk of 256 (32 state intervals):
-    # the result is the same up to rounding; the automatic row chunk (512)
-    # writes half the state snapshots.
+    # the result is the same up to rounding; the automatic row chunk (1024)
+    # writes a quarter of the state snapshots.
     for _ in range(2):
         lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho, chunk=C)
     e0.record()
@@ -246,20 +246,20 @@ def bench_long(torch, args):
     k_flop = B * H * T * (4 * N * D + (C - 1) * N)
     achieved = k_flop / (k_ms * 1e-3) / 1e12
     print(f"[long] {ms:.3f} ms/prefill, {B * T / (ms * 1e-3) / 1e6:.2f} M tok/s, "
-          f"{call_tflops:.1f} TFLOP/s per call; carry + prefill_mfma kernels {k_n:.0f} launches, "
+          f"{call_tflops:.1f} TFLOP/s per call; carry + snap_wide kernels {k_n:.0f} launches, "
           f"{k_ms:.3f} ms, {achieved:.1f} TFLOP/s; at row chunk {C}: {ms_c:.3f} ms", flush=True)
     return {"metric": "C4 long-context prefill tokens/s per BDH layer", "value": B * T / (ms * 1e-3),
             "unit": "tokens/s", "ms_per_prefill": ms, "steps": steps,
             "config": {"workload": "C4 long prefill, one BDH layer: B1 nh4 T8192 N8192 D256, "
                                    "bf16 in / fp32 acc, RoPE fused; automatic row chunk (rho "
-                                   "snapshots every 512 tokens), credited at the config's "
+                                   "snapshots every 1024 tokens), credited at the config's "
                                    f"chunk {C}"},
             "at_config_chunk": {"chunk": C, "ms_per_prefill": round(ms_c, 4),
                                 "tokens_per_s": round(B * T / (ms_c * 1e-3), 1)},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                          "traffic": TRAFFIC_LONG_C4,
-                         "kernel": f"prefill_carry_kernel + prefill_mfma_kernel, {k_n:.0f} launches "
+                         "kernel": f"prefill_carry_kernel + snap_wide_kernel, {k_n:.0f} launches "
                                    "per call (summed)",
                          "kernel_ms_per_call": round(k_ms, 4), "flop_per_call": k_flop,
                          "call": {"tflops": round(call_tflops, 2), "flop": flop, "traffic": TRAFFIC_LONG_C4_CALL}}}

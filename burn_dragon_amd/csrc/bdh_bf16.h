@@ -150,7 +150,7 @@ struct PrefillArgs {
   int64_t L, Lp, n_iv;
   int ks, nb;           // N splits (N/32 a multiple of 4 ks); 256-row blocks per interval
   int gram_groups;      // S * ks * n_iv
-  int gram_ids;         // workgroup ids of the gram groups (prefill_gram_ids), readout tiles included
+  int gram_ids;         // workgroup ids of the gram groups (prefill_gram_ids / snap_wide_ids)
   // state units
   const bf16_t* vt;     // v^T [B*Hv, Tp/32, Dp, 32] (step-major), zero past (D, T); Dp = D rounded up to 256
   const float* rho_in;  // [S, N, D] or null
@@ -172,10 +172,10 @@ struct PrefillArgs {
   float* add_ctx;       // [S, T, D]
   int64_t add_t0, add_Lc;
   int add_units;
-  // snapshot mode (rd_snap set; x pre-rotated, no decay): rd_pg readout
-  // tiles per gram group, for every interval iv >= rd_iv0, over the group's
-  // N range (rd_kr = ks): rd_part [rd_kr, S, T, D] = q rho_iv, rho_iv from
-  // rd_snap [n_iv, S, D, N] bf16 (prefill_carry_kernel)
+  // snapshot mode (snap_wide.hip; rd_snap set, x pre-rotated, no decay):
+  // rd_pg readout tiles per gram group, for every interval iv >= rd_iv0, over
+  // the group's N range (rd_kr = ks): rd_part [rd_kr, S, T, D] = q rho_iv,
+  // rho_iv from rd_snap [n_iv, S, D, N] bf16 (prefill_carry_kernel)
   const bf16_t* rd_snap;
   int64_t rd_iv0;
   int rd_pg;
@@ -200,6 +200,12 @@ struct CarryArgs {
   bf16_t* q;            // [S, T, N] rotated queries (freqs set)
 };
 int prefill_carry_units(int64_t S, int64_t N, int64_t Dp);
+// Gram and readout tiles of the state-carry form in 8-wave workgroups
+// (snap_wide.hip): PrefillArgs in snapshot mode (rd_snap, rd_iv0, rd_pg =
+// readout tiles per group = 256-row blocks x 256-column blocks, rd_kr = ks),
+// gram_ids = snap_wide_ids(groups, nb, rd_pg).
+int snap_wide_ids(int groups, int nb, int rd_pg);
+hipError_t launch_snap_wide(const PrefillArgs& a, hipStream_t st);
 hipError_t launch_prefill_carry(const CarryArgs& a, hipStream_t st);
 
 // RoPE position of token t of the call (attention.rs:488-501 with the
@@ -232,7 +238,7 @@ __device__ __forceinline__ uint4 rope_cs4(float p, const float (&f)[4]) {
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
 // Workgroup ids a gram launch needs for `groups` groups of nb-block
 // intervals (ids are laid out so that one group's tiles share an XCD).
-int prefill_gram_ids(int groups, int nb, int rd_pg = 0);
+int prefill_gram_ids(int groups, int nb);
 // State units of one interval.
 int prefill_state_units(int64_t S, int64_t N, int64_t D);
 // Readout units of one interval of Lc rows.

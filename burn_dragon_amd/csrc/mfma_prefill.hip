@@ -423,79 +423,6 @@ __device__ __forceinline__ void readout_unit(const PrefillArgs& a, bf16_t* lds, 
 }
 
 // ---------------------------------------------------------------------------
-// readout unit over a bf16 state snapshot: rd_part[kp, s, t0 + r, d] =
-// sum over the kp-th N range of q[s, t0 + r, n] rho_iv[n, d] for rows
-// r0 .. r0+255 of interval iv (t0 = iv L) and columns d0 .. d0+127.  Both
-// operands are k-contiguous bf16 rows (q rows; rho_iv^T rows of snap[iv]),
-// so they are fetched straight into a three-stage LDS ring two steps ahead,
-// as the rotation-free gram tiles do.  Stage rows: q rows 0..255, then
-// rho^T rows 256..383.  Rows past a ragged interval re-read its last row,
-// columns past D re-read column D - 1; neither is stored.
-template <bool WHOLE>
-__device__ __forceinline__ void readout_snap_unit(const PrefillArgs& a, bf16_t* lds, int64_t s, int kp,
-                                                  int64_t iv, int64_t r0, int64_t d0) {
-  const int lane = threadIdx.x & 63, w = wave_id();
-  const int64_t t0 = iv * a.L;
-  const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
-  const int64_t rowb = a.N * 2;  // bytes per q row and per rho^T row
-  const char* X = reinterpret_cast<const char*>(a.x + (s * a.T + t0) * a.N);
-  const char* R = reinterpret_cast<const char*>(a.rd_snap + (iv * a.S + s) * a.D * a.N);
-  const int nk = (int)(a.N / BK);
-  const int kb = (int)((int64_t)nk * kp / a.rd_kr), ke = (int)((int64_t)nk * (kp + 1) / a.rd_kr);
-  constexpr int groups = 6;
-  const uint32_t gc = (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
-  uint32_t voff[groups];
-  int64_t vbase[groups];
-#pragma unroll
-  for (int j = 0; j < groups; ++j) {
-    // Wave w fetches rows 16 w .. 16 w + 15 of group j (stage block w + 4 j).
-    if (j < 4) {
-      const int64_t rr = r0 + 64 * j + 16 * w;
-      if (WHOLE) {
-        vbase[j] = rr * rowb;
-        voff[j] = (uint32_t)((lane >> 2) * rowb) + gc * 16;
-      } else {
-        const int64_t t = rr + (lane >> 2);
-        vbase[j] = 0;
-        voff[j] = (uint32_t)((t < Lc ? t : Lc - 1) * rowb) + gc * 16;
-      }
-    } else {
-      const int64_t d = d0 + 64 * (j - 4) + 16 * w + (lane >> 2);
-      vbase[j] = 0;
-      voff[j] = (uint32_t)((d < a.D ? d : a.D - 1) * rowb) + gc * 16;
-    }
-  }
-  constexpr int STAGE = groups * 64 * BK;  // bf16 elements of one stage
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-  auto issue = [&](int kt, int stg) {
-    const int64_t kofs = (int64_t)kt * 64;
-#pragma unroll
-    for (int j = 0; j < groups; ++j)
-      dma16((j < 4 ? X : R) + vbase[j] + kofs, voff[j], lds0 + (uint32_t)(stg * STAGE * 2 + (w + 4 * j) * 1024));
-  };
-  floatx4 acc[4][8];
-  zero_acc(acc);
-  const bool active = r0 + 64 * w < Lc;
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): see the gram ring
-  issue(kb, 0);
-  issue(kb + 1 < ke ? kb + 1 : kb, 1);
-  int stg = 0;
-  for (int kt = kb; kt < ke; ++kt) {
-    dma_wait_barrier<groups>();
-    issue(kt + 2 < ke ? kt + 2 : ke - 1, stg == 0 ? 2 : stg - 1);
-    if (active) mma_64x128_dsasm(lds + stg * STAGE, lds + stg * STAGE, lane, 64 * w, T256, acc);
-    stg = stg == 2 ? 0 : stg + 1;
-  }
-  dma_wait_barrier<0>();  // the epilogue reuses the ring
-  float* P = a.rd_part + ((int64_t)kp * a.S + s) * a.T * a.D + t0 * a.D;
-  epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
-    const int64_t t = r0 + 64 * w + row, d = d0 + col;
-    if (t < Lc && d < a.D)
-      __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, reinterpret_cast<floatx4*>(&P[t * a.D + d]));
-  });
-}
-
-// ---------------------------------------------------------------------------
 // add unit aid: a contiguous share of the previous interval's (s, t, float4)
 // context elements; the partials are summed in split order onto ctx (the
 // order of readout_add_kernel).
@@ -559,9 +486,9 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[3 * BUF];
   const int id = blockIdx.x;
   if (id < a.gram_ids) {
-    const int tpg = units_per_group(a.nb) + a.rd_pg;
+    const int tpg = units_per_group(a.nb);
     const int blk = id / (8 * tpg), rem = id - blk * 8 * tpg;
-    int u = rem >> 3;
+    const int u = rem >> 3;
     const int g = blk * 8 + (rem & 7);
     if (g >= a.gram_groups) return;
     const int64_t iv = g % a.n_iv;
@@ -570,21 +497,6 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
     const int64_t s = q / a.ks;
     const int64_t t0 = iv * a.L;
     const int64_t Lc = (a.T - t0 < a.L) ? a.T - t0 : a.L;
-    if (u < a.rd_pg) {
-      // Readout tiles of the group's interval and N range (snapshot mode):
-      // they read the same q rows as the group's gram tiles, at the same time
-      // and on the same XCD, so those rows come from L2 rather than HBM.
-      if constexpr (!ROPE && !DECAY) {
-        if (iv < a.rd_iv0) return;
-        const int ndb = (int)((a.D + T256 / 2 - 1) / (T256 / 2));
-        const int64_t r0 = (int64_t)(u / ndb) * T256, d0 = (int64_t)(u % ndb) * (T256 / 2);
-        if (r0 >= Lc) return;  // past a ragged last interval
-        if (r0 + T256 <= Lc) readout_snap_unit<true>(a, lds, s, kp, iv, r0, d0);
-        else readout_snap_unit<false>(a, lds, s, kp, iv, r0, d0);
-      }
-      return;
-    }
-    u -= a.rd_pg;
     if (u >= a.nb * a.nb) {
       // Pair of diagonal blocks of row blocks 2j and 2j + 1.
       const int j = u - a.nb * a.nb;
@@ -643,8 +555,8 @@ __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
 
 }  // namespace
 
-int prefill_gram_ids(int groups, int nb, int rd_pg) {
-  const int tpg = nb * nb + (nb + 1) / 2 + rd_pg;
+int prefill_gram_ids(int groups, int nb) {
+  const int tpg = nb * nb + (nb + 1) / 2;
   return ((groups + 7) / 8) * 8 * tpg;
 }
 

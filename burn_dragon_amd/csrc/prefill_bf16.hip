@@ -381,18 +381,21 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   const bool rope = a.freqs != nullptr;
   const int64_t L = a.L;
   const int64_t rd_iv0 = a.rho_in ? 0 : 1;
-  const int ndb = (int)cdiv(a.D, T256 / 2);
-  // The readout tiles of an interval join its gram group (same N range, same
+  // Gram and readout tiles run in 8-wave workgroups (snap_wide.hip, one per
+  // CU); an interval's readout tiles join its gram group (same N range, same
   // XCD, dispatched together): they read the same q rows.  N splits: 1 or 2,
-  // whichever gives the fewer steps in rounds of units over the workgroup
-  // slots (two per CU), 1 on a tie (every split writes, and the context
-  // kernel re-reads, one more set of partials).  Measured at C4, chunk 512:
-  // 576 units of 256 steps take 2 rounds, 1152 of 128 steps 3 (0.85 against
-  // 0.875 ms per call); 4 splits were slower at every chunk.
-  const int64_t slots = 2 * (int64_t)device_cus();
-  const int64_t upg = (int64_t)nb * nb + (nb + 1) / 2 + (int64_t)nb * ndb;
+  // whichever gives the fewer steps in rounds of units over the CUs, 1 on a
+  // tie (every split writes, and the context kernel re-reads, one more set
+  // of partials).  Measured at C4: chunk 1024 (a tie) 0.83 ms with 1 split,
+  // 0.88 with 2; chunk 512 0.875 with 2, 0.889 with 1; 4 splits (the fewest
+  // rounds at 512 and 1024) made the context kernel read twice as much
+  // (chunk 512: 157 against 58 us) and the call 0.93-0.98 ms.
+  const int ndb256 = (int)cdiv(a.D, T256);
+  const int rd_pg = nb * ndb256;
+  const int64_t slots = device_cus();
+  const int64_t upg = (int64_t)nb * (nb - 1) / 2 + nb + rd_pg;
   auto rounds = [&](int k) { return (S * n_iv * k * upg + slots - 1) / slots * (nk / k); };
-  const int ks = (nk % 4 == 0 && rounds(2) < rounds(1)) ? 2 : 1;
+  const int ks = (nk % 2 == 0 && rounds(2) < rounds(1)) ? 2 : 1;
   const int kr = ks;
 
   void *vt = nullptr, *part = nullptr, *snap = nullptr, *rdp = nullptr, *q = nullptr;
@@ -439,8 +442,8 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   p.L = L; p.Lp = Lp; p.n_iv = n_iv;
   p.ks = ks; p.nb = nb;
   p.gram_groups = (int)(S * ks * n_iv);
-  p.rd_pg = nb * ndb;
-  p.gram_ids = prefill_gram_ids(p.gram_groups, nb, p.rd_pg);
+  p.rd_pg = rd_pg;
+  p.gram_ids = snap_wide_ids(p.gram_groups, nb, p.rd_pg);
   p.vt = (const bf16_t*)vt;
   p.Tp = Tp; p.Dp = Dp;
   p.state_units = 0;
@@ -451,7 +454,7 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   p.rd_iv0 = rd_iv0;
   p.add_units = 0;
   kt = ktime_begin(BDH_KERNEL_PREFILL, st);
-  BDH_HIP_TRY(launch_prefill_mfma(p, false, st));
+  BDH_HIP_TRY(launch_snap_wide(p, st));
   ktime_end(kt, st);
 
   CtxArgs cx{(const bf16_t*)vt, (const float*)part, a.ctx, a.H, a.Hv, a.T, a.D, L, Lp, Tp, Dp, S,
