@@ -6,6 +6,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "bdh_bf16.h"
 
@@ -213,6 +214,60 @@ __device__ __forceinline__ void mma_64x128_dsasm(const bf16_t* A, const bf16_t* 
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
     for (int ni = 4; ni < 8; ++ni) mm(mi, ni);
+}
+
+// Cross-step form of mma_64x128_dsasm for rings whose next stage is known to
+// have landed while the current one is multiplied:
+//   frags_64x128_wait(f)        f (read one step earlier) has arrived: all of
+//                               the wave's LDS reads are waited for, so no
+//                               more than 12 are ever in flight;
+//   frag_64x128_read<I>(a, b, g)  starts fragment read I (0..3: A rows
+//                               16 I.., 4..11: B rows 16 (I - 4)..) of the
+//                               next step, a and b from frag_64x128_base;
+//   mma_64x128_frags(f, acc, between)
+//                               the step's 32 MFMAs in 8 groups of 4 (one B
+//                               fragment each); between(integral_constant<G>)
+//                               runs after group G, fenced so that the
+//                               scheduler keeps it there.
+// A caller spreads the next step's fragment reads (and its DMAs) over the
+// groups: issued together after a barrier, 8 waves' reads (96 KiB) queue in
+// the LDS for hundreds of cycles, and each wave's MFMAs wait behind its own
+// reads' issue.
+__device__ __forceinline__ uint32_t frag_64x128_base(const bf16_t* M, int lane, int row) {
+  return lds_addr(M) + (uint32_t)(2 * lds_off(row + (lane & 15), lane >> 4));
+}
+template <int I>
+__device__ __forceinline__ void frag_64x128_read(uint32_t a, uint32_t b, u32x4 (&af)[4], u32x4 (&bf)[8]) {
+  if constexpr (I < 4)
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[I]) : "v"(a), "n"(I * 1024));
+  else
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[I - 4]) : "v"(b), "n"((I - 4) * 1024));
+}
+__device__ __forceinline__ void frags_64x128_wait(u32x4 (&af)[4], u32x4 (&bf)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(af[0]), "+v"(af[1]), "+v"(af[2]), "+v"(af[3]), "+v"(bf[0]), "+v"(bf[1]), "+v"(bf[2]),
+                 "+v"(bf[3]), "+v"(bf[4]), "+v"(bf[5]), "+v"(bf[6]), "+v"(bf[7]));
+}
+template <int G, class Between>
+__device__ __forceinline__ void mma_64x128_group(const u32x4 (&af)[4], const u32x4 (&bf)[8], floatx4 (&acc)[4][8],
+                                                 Between& between) {
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+    acc[mi][G] = mfma16(__builtin_bit_cast(bf16x8, af[mi]), __builtin_bit_cast(bf16x8, bf[G]), acc[mi][G]);
+  __builtin_amdgcn_sched_barrier(0);
+  between(std::integral_constant<int, G>{});
+  __builtin_amdgcn_sched_barrier(0);
+}
+template <class Between, int... G>
+__device__ __forceinline__ void mma_64x128_groups(const u32x4 (&af)[4], const u32x4 (&bf)[8], floatx4 (&acc)[4][8],
+                                                  Between& between, std::integer_sequence<int, G...>) {
+  (mma_64x128_group<G>(af, bf, acc, between), ...);
+}
+template <class Between>
+__device__ __forceinline__ void mma_64x128_frags(u32x4 (&af)[4], u32x4 (&bf)[8], floatx4 (&acc)[4][8],
+                                                 Between&& between) {
+  __builtin_amdgcn_sched_barrier(0);
+  mma_64x128_groups(af, bf, acc, between, std::make_integer_sequence<int, 8>{});
 }
 
 }  // namespace mfma

@@ -13,12 +13,16 @@
 //     transposed ([d][n]: the operand layout of the readout units);
 //   - at the end it writes the final rho in f32.
 // The readouts of every interval and the gram tiles then run in one launch
-// (prefill_mfma_kernel), with no chain of per-interval launches and no f32
+// (snap_wide_kernel), with no chain of per-interval launches and no f32
 // state round trips between intervals.
 //
-// Loads run P steps ahead in registers (one workgroup per CU when the call
-// has few streams, so the loads, not a second workgroup, hide the latency);
-// LDS double-buffers one step's q^T and v^T.
+// Roles (512 threads, 8 waves, one workgroup per CU): waves 0..3 own the
+// 64 x 128 accumulator blocks, multiply and store q; waves 4..7 fetch x and
+// v^T (direct-to-LDS ring) and rotate x.  With one barrier per 32-token
+// step, a SIMD's multiplying wave runs its MFMAs while its loading wave does
+// the rotation's VALU and LDS work.  The loading waves issue loads only, so
+// their waits can count DMAs in flight (loads complete in order; a store
+// issued later may complete before them).
 #include "bdh_mfma.h"
 
 namespace bdh {
@@ -26,52 +30,64 @@ namespace {
 
 using namespace mfma;
 
+constexpr int CARRY_NT = 512;
 constexpr int CARRY_N = T256 / 2;  // neurons per block
-constexpr int CARRY_R = 5;         // ring stages: loads run CARRY_R - 2 steps ahead
+constexpr int CARRY_R = 5;         // ring stages
 // LDS bytes: ring stages of raw x [32 tokens][128 neurons] (8 KiB) + v^T
 // [256 columns][32 tokens] (16 KiB), then the double-buffered q^T [128][32].
 constexpr int CARRY_STAGE = 24 * 1024;
 constexpr int CARRY_XT = CARRY_R * CARRY_STAGE;
 constexpr int CARRY_LDS = CARRY_XT + 2 * 8 * 1024;
-// Vector memory operations a wave issues per step: 2 x DMAs + 4 v^T DMAs,
-// plus its 2 q stores when it writes q.  Waiting for at most 18 in flight at
-// the start of step k leaves stage k landed: in steady state 2 + 2 x 8 (or
-// 2 x 6) operations follow stage k's DMAs; in the first steps (stages issued
-// by the prologue, 6 each) at least 18.  With q stores the wait also covers
-// one step more than needed (the ring then runs 2 steps ahead, not 3).
-constexpr int CARRY_WAIT = 18;
 
+// Step k (one barrier B_k at its start):
+//   loaders   DMA of step k + 4 into the slot of step k - 1, then x of step
+//             k + 1 rotated: q^T into buffer (k + 1) & 1 and (with q) q back
+//             in place in its slot;
+//   multiply  q^T buffer k & 1 x v^T of slot k into the accumulators, then
+//             q of step k (rotated during step k - 1) from slot k to HBM.
+// B_k needs stage k + 1 landed (its x is rotated during step k) and every
+// LDS access of step k - 1 finished: slot k - 1 and q^T buffer (k + 1) & 1
+// are rewritten during step k.  A loading wave issues 6 DMAs per step;
+// stage k + 1's (step k - 3) are followed by those of steps k - 2 and k - 1,
+// so waiting for at most 12 in flight leaves it landed (steps 1 and 2 need
+// prologue stages only, all waited for).
+constexpr int CARRY_WAIT = 12;
+
+template <int N>
+__device__ __forceinline__ void lds_dma_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void plain_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// The loading waves (rw = wave - 4).
 template <bool ROPE, bool QOUT>
-__device__ __forceinline__ void carry_unit(const CarryArgs& a, char* lds, int64_t s, int64_t n0,
-                                           int64_t d0) {
-  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-  const int wm = w >> 1, wn = w & 1;  // n rows 64 wm .., d columns 128 wn ..
+__device__ __forceinline__ void carry_loader(const CarryArgs& a, char* lds, int64_t s, int64_t n0, int64_t d0,
+                                             int rw, int lane) {
+  const int rtid = rw * 64 + lane;
   const int64_t b = s / a.H, h = s - b * a.H;
   const int64_t rowb = a.N * 2;  // bytes per x row
   const char* X = reinterpret_cast<const char*>(a.x + s * a.T * a.N);
   const char* VT = reinterpret_cast<const char*>(a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp) + d0 * 64;
-  bf16_t* Q = QOUT ? a.q + s * a.T * a.N : nullptr;
   const int64_t vstep = a.Dp * 64;  // bytes of one 32-token step of v^T
   const int nk = (int)(a.Tp / BK);  // a multiple of 4 (Tp: T rounded up to 128)
-  const int spi = (int)(a.L / BK);  // steps per interval
 
-  // DMA lanes.  x: 1 KiB blocks of 4 rows x 256 bytes (128 neurons); wave w
-  // fetches blocks w and w + 4; LDS chunk c of row r holds global chunk
+  // DMA lanes.  x: 1 KiB blocks of 4 rows x 256 bytes (128 neurons); wave rw
+  // fetches blocks rw and rw + 4; LDS chunk c of row r holds global chunk
   // c ^ (r & 15), so that the readers below (16 rows, one chunk column) hit
-  // distinct banks.  v^T: 1 KiB blocks of 16 rows x 64 bytes, blocks w + 4 j;
+  // distinct banks.  v^T: 1 KiB blocks of 16 rows x 64 bytes, blocks rw + 4 j;
   // the lane writing slot c of row r fetches chunk c ^ ((r >> 1) & 3), the
   // swizzle of the MFMA operand layout (lds_off).
   int xrow[2];
   uint32_t xcol[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    xrow[j] = 4 * (w + 4 * j) + (lane >> 4);
+    xrow[j] = 4 * (rw + 4 * j) + (lane >> 4);
     xcol[j] = (uint32_t)((n0 + 8 * ((lane & 15) ^ (xrow[j] & 15))) * 2);
   }
   uint32_t voff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int r = 16 * (w + 4 * j) + (lane >> 2);
+    const int r = 16 * (rw + 4 * j) + (lane >> 2);
     voff[j] = (uint32_t)(r * 64 + (((lane & 3) ^ ((r >> 1) & 3)) * 16));
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
@@ -81,41 +97,38 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, char* lds, int64_
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int64_t t = tb + xrow[j];
-      dma16(X, (uint32_t)((t < a.T ? t : a.T - 1) * rowb) + xcol[j], base + (uint32_t)((w + 4 * j) * 1024));
+      dma16(X, (uint32_t)((t < a.T ? t : a.T - 1) * rowb) + xcol[j], base + (uint32_t)((rw + 4 * j) * 1024));
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      dma16(VT + (int64_t)kt * vstep, voff[j], base + 8192u + (uint32_t)((w + 4 * j) * 1024));
+      dma16(VT + (int64_t)kt * vstep, voff[j], base + 8192u + (uint32_t)((rw + 4 * j) * 1024));
   };
 
   // Rotation lanes: tokens 2 tp, 2 tp + 1 of the step x neurons n0 + 8 nv ..
-  const int tp = tid & 15, nv = tid >> 4;
+  const int tp = rtid & 15, nv = rtid >> 4;
   float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (ROPE) load_freq4(a.freqs + n0 + 8 * nv, fq);
   // q^T of step k (tokens 2 tp, 2 tp + 1 of neuron 8 nv + e) into buffer k & 1.
   auto rotate = [&](int kt, int slot) {
-    const char* R = lds + slot * CARRY_STAGE;
+    char* R = lds + slot * CARRY_STAGE;
     const int r0 = 2 * tp, r1 = 2 * tp + 1;
-    uint4 q0 = *reinterpret_cast<const uint4*>(R + r0 * 256 + ((nv ^ (r0 & 15)) << 4));
-    uint4 q1 = *reinterpret_cast<const uint4*>(R + r1 * 256 + ((nv ^ (r1 & 15)) << 4));
-    // Tokens past T hold row T - 1 (see issue) and are rotated at its
-    // position, so their q is row T - 1's and is stored there again (the same
-    // bytes); their v^T columns are zero, so they add nothing to rho.
-    const int64_t t = (int64_t)kt * BK + 2 * tp;
-    const int64_t ta = t < a.T ? t : a.T - 1, tb = t + 1 < a.T ? t + 1 : a.T - 1;
+    uint4* X0 = reinterpret_cast<uint4*>(R + r0 * 256 + ((nv ^ (r0 & 15)) << 4));
+    uint4* X1 = reinterpret_cast<uint4*>(R + r1 * 256 + ((nv ^ (r1 & 15)) << 4));
+    uint4 q0 = *X0, q1 = *X1;
     if (ROPE) {
-      // Sums of integers below 2^24 are exact in f32.
+      // Tokens past T hold row T - 1 (see issue) and are rotated at its
+      // position, so their q is row T - 1's; their v^T columns are zero, so
+      // they add nothing to rho.  Sums of integers below 2^24 are exact in f32.
+      const int64_t t = (int64_t)kt * BK + 2 * tp;
+      const int64_t ta = t < a.T ? t : a.T - 1, tb = t + 1 < a.T ? t + 1 : a.T - 1;
       const float pa = (float)(a.fixed ? a.pos0 : a.pos0 + ta);
       const float pb = (float)(a.fixed ? a.pos0 : a.pos0 + tb);
       q0 = rot8_bf16(q0, rope_cs4(pa, fq));
       q1 = rot8_bf16(q1, rope_cs4(pb, fq));
     }
-    if (QOUT) {
-      // Read by the next launch after ~1 GB of other traffic: streaming stores.
-      __builtin_nontemporal_store(u32x4{q0.x, q0.y, q0.z, q0.w},
-                                  reinterpret_cast<u32x4*>(Q + ta * a.N + n0 + 8 * nv));
-      __builtin_nontemporal_store(u32x4{q1.x, q1.y, q1.z, q1.w},
-                                  reinterpret_cast<u32x4*>(Q + tb * a.N + n0 + 8 * nv));
+    if (QOUT) {  // back in place for the q stores (each thread rewrites only what it read)
+      *X0 = q0;
+      *X1 = q1;
     }
     // q^T: word (neuron e, tokens 2 tp, 2 tp + 1) from the two tokens' words.
     const uint32_t u0[4] = {q0.x, q0.y, q0.z, q0.w}, u1[4] = {q1.x, q1.y, q1.z, q1.w};
@@ -126,7 +139,32 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, char* lds, int64_
       Aw[(lds_off(8 * nv + 2 * p + 1, tp >> 2) + 2 * (tp & 3)) >> 1] = (u0[p] >> 16) | (u1[p] & 0xffff0000u);
     }
   };
+  // Every load above has completed before the ring starts (the compiler cannot
+  // see the DMAs, so it must not be left waiting for older loads inside it).
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+#pragma unroll
+  for (int j = 0; j < CARRY_R - 1; ++j) issue(j, j);  // nk >= 4 = CARRY_R - 1
+  lds_dma_wait_barrier<0>();                          // prologue stages landed
+  rotate(0, 0);
+  for (int k = 0; k < nk; ++k) {
+    lds_dma_wait_barrier<CARRY_WAIT>();  // B_k
+    // Step k + 4 into the slot of step k - 1; past the end the last step is
+    // fetched again (unused), so every step issues the same operations.
+    issue(k + CARRY_R - 1 < nk ? k + CARRY_R - 1 : nk - 1, (k + CARRY_R - 1) % CARRY_R);
+    if (k + 1 < nk) rotate(k + 1, (k + 1) % CARRY_R);
+  }
+  lds_dma_wait_barrier<0>();  // the epilogue reuses the ring
+#pragma unroll
+  for (int i = 0; i < 8; ++i) __syncthreads();  // the multiplying waves' epilogue barriers
+}
 
+// The multiplying waves (w = 0..3): rows n0 + 64 wm .., columns d0 + 128 wn ..
+template <bool QOUT>
+__device__ __forceinline__ void carry_mma(const CarryArgs& a, char* lds, int64_t s, int64_t n0, int64_t d0, int w,
+                                          int lane) {
+  const int wm = w >> 1, wn = w & 1;
+  const int nk = (int)(a.Tp / BK);  // a multiple of 4 (Tp: T rounded up to 128)
+  const int spi = (int)(a.L / BK);  // steps per interval
   const bool active = d0 + 128 * wn < a.D;
   floatx4 acc[4][8];
   // Accumulator element (mi, ni, r): n = n0 + 64 wm + 16 mi + 4 (lane >> 4) + r,
@@ -164,31 +202,39 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, char* lds, int64_
       }
   };
   if (a.rho_in) snapshot(0);
-
-  // Every load above has completed before the ring starts (the compiler cannot
-  // see the DMAs, so it must not be left waiting for older loads inside it).
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  bf16_t* Q = QOUT ? a.q + s * a.T * a.N : nullptr;
+  // q rows of step k from its ring slot (rotated in place) to HBM: lane
+  // (lane & 15) stores chunk c of rows 4 (w + 4 j) + (lane >> 4), so each
+  // store instruction writes 4 whole 256-byte row pieces (the rotation
+  // lanes' own layout would write 64-byte pieces, each 128-byte line then
+  // completed by another wave later, which costs HBM write bytes).  Rows
+  // past T hold row T - 1's q and are stored there again (the same bytes).
+  auto store_q = [&](int kt, int slot) {
+    const char* R = lds + slot * CARRY_STAGE;
+    const int c = lane & 15;
 #pragma unroll
-  for (int j = 0; j < CARRY_R - 1; ++j) issue(j, j);  // nk >= 4 = CARRY_R - 1
-  int slot = 0;  // ring slot of step k
+    for (int j = 0; j < 2; ++j) {
+      const int r = 4 * (w + 4 * j) + (lane >> 4);
+      const uint4 v = *reinterpret_cast<const uint4*>(R + r * 256 + ((c ^ (r & 15)) << 4));
+      const int64_t t = (int64_t)kt * BK + r;
+      // Read by the next launch after ~1 GB of other traffic: streaming stores.
+      __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w},
+                                  reinterpret_cast<u32x4*>(Q + (t < a.T ? t : a.T - 1) * a.N + n0 + 8 * c));
+    }
+  };
+
+
+  plain_barrier();  // the loaders' prologue stages landed
   for (int k = 0; k < nk; ++k) {
-    // Stage k has landed for every wave, and every wave has finished the LDS
-    // reads of step k - 1 (slot k - 1 and the q^T buffer of step k - 1 are free).
-    dma_wait_barrier<CARRY_WAIT>();
-    // Step k + CARRY_R - 1 into slot k - 1; past the end the last step is
-    // fetched again (unused), so every step issues the same operations.
-    const int nxt = k + CARRY_R - 1 < nk ? k + CARRY_R - 1 : nk - 1;
-    issue(nxt, slot == 0 ? CARRY_R - 1 : slot - 1);
-    rotate(k, slot);
-    __syncthreads();  // q^T of step k written
+    plain_barrier();  // B_k: q^T of step k written, stage k landed
     if (active)
       mma_64x128_dsasm(reinterpret_cast<const bf16_t*>(lds + CARRY_XT + (k & 1) * 8192),
-                       reinterpret_cast<const bf16_t*>(lds + slot * CARRY_STAGE + 8192), lane, 64 * wm,
+                       reinterpret_cast<const bf16_t*>(lds + (k % CARRY_R) * CARRY_STAGE + 8192), lane, 64 * wm,
                        128 * wn, acc);
-    slot = slot == CARRY_R - 1 ? 0 : slot + 1;
+    if (QOUT) store_q(k, k % CARRY_R);
     if ((k + 1) % spi == 0 && k + 1 < nk) snapshot((k + 1) / spi);
   }
-  dma_wait_barrier<0>();  // the epilogue reuses the ring
+  lds_dma_wait_barrier<0>();  // the epilogue reuses the ring
 
   epilogue_64x128(acc, reinterpret_cast<bf16_t*>(lds), w, lane, [&](int row, int col, float4 v) {
     const int64_t n = n0 + 64 * wm + row, d = d0 + 128 * wn + col;
@@ -198,8 +244,15 @@ __device__ __forceinline__ void carry_unit(const CarryArgs& a, char* lds, int64_
   });
 }
 
+template <bool ROPE, bool QOUT>
+__device__ __forceinline__ void carry_unit(const CarryArgs& a, char* lds, int64_t s, int64_t n0, int64_t d0) {
+  const int lane = threadIdx.x & 63, w = wave_id();
+  if (w >= 4) carry_loader<ROPE, QOUT>(a, lds, s, n0, d0, w - 4, lane);
+  else carry_mma<QOUT>(a, lds, s, n0, d0, w, lane);
+}
+
 template <bool ROPE>
-__global__ __launch_bounds__(NT, 1) void prefill_carry_kernel(CarryArgs a) {
+__global__ __launch_bounds__(CARRY_NT, 1) void prefill_carry_kernel(CarryArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[CARRY_LDS];
   const int nt = (int)(a.N / CARRY_N);
   const int dt = (int)(a.Dp / T256);
@@ -222,8 +275,8 @@ int prefill_carry_units(int64_t S, int64_t N, int64_t Dp) { return (int)(S * (N 
 
 hipError_t launch_prefill_carry(const CarryArgs& a, hipStream_t st) {
   const unsigned grid = (unsigned)prefill_carry_units(a.S, a.N, a.Dp);
-  if (a.freqs) hipLaunchKernelGGL((prefill_carry_kernel<true>), dim3(grid), dim3(NT), 0, st, a);
-  else hipLaunchKernelGGL((prefill_carry_kernel<false>), dim3(grid), dim3(NT), 0, st, a);
+  if (a.freqs) hipLaunchKernelGGL((prefill_carry_kernel<true>), dim3(grid), dim3(CARRY_NT), 0, st, a);
+  else hipLaunchKernelGGL((prefill_carry_kernel<false>), dim3(grid), dim3(CARRY_NT), 0, st, a);
   return hipGetLastError();
 }
 

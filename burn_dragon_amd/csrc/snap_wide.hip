@@ -1,7 +1,7 @@
 // Gram and readout tiles of the state-carry form (two or more intervals, no
 // decay, q already rotated) in 512-thread workgroups (8 waves, one per CU).
 //
-// Every operand row comes from HBM (or L2) through a three-stage direct-load
+// Every operand row comes from HBM (or L2) through a four-stage direct-load
 // LDS ring, so what bounds these tiles is the operand traffic per MFMA.  A
 // wave owns a 64 x 128 block of v_mfma_f32_16x16x32_bf16 accumulators, and
 // the workgroup's 4 x 2 waves cover a 256 x 256 tile:
@@ -28,7 +28,7 @@ using namespace mfma;
 
 constexpr int SW_NT = 512;                  // 8 waves
 constexpr int SW_STAGE = 2 * T256 * BK;     // bf16 elements of one stage: 512 rows of 32
-constexpr int SW_LDS = 3 * SW_STAGE;        // three stages (96 KiB); the epilogue reuses them
+constexpr int SW_LDS = 4 * SW_STAGE;        // four stages (128 KiB); the epilogue reuses them
 
 enum { K_DIAG = 0, K_OFF = 1, K_READ = 2 };
 
@@ -77,12 +77,13 @@ __device__ __forceinline__ void snap_wide_unit(const PrefillArgs& a, bf16_t* lds
     }
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  auto issue1 = [&](int kt, int stg, int j) {
+    dma16((KIND == K_READ && j >= 2 ? R : X) + vbase[j] + (int64_t)kt * 64, voff[j],
+          lds0 + (uint32_t)(stg * SW_STAGE * 2 + (w + 8 * j) * 1024));
+  };
   auto issue = [&](int kt, int stg) {
-    const int64_t kofs = (int64_t)kt * 64;
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-      dma16((KIND == K_READ && j >= 2 ? R : X) + vbase[j] + kofs, voff[j],
-            lds0 + (uint32_t)(stg * SW_STAGE * 2 + (w + 8 * j) * 1024));
+    for (int j = 0; j < NB; ++j) issue1(kt, stg, j);
   };
 
   floatx4 acc[4][8];
@@ -94,18 +95,82 @@ __device__ __forceinline__ void snap_wide_unit(const PrefillArgs& a, bf16_t* lds
   else active = wr0 < Lc && wc0 < a.D;
   const int brow = KIND == K_DIAG ? 128 * wc : T256 + 128 * wc;
 
+  // Ring of 4 stages, step kt in stage (kt - kb) & 3.  At step kt the barrier
+  // confirms stage kt + 1 (DMAs issued two steps earlier); each wave then
+  // starts the fragment reads of step kt + 1 and multiplies step kt from the
+  // fragments it read during step kt - 1, so LDS reads overlap MFMAs.  The
+  // DMA of step kt + 3 goes into the stage of step kt - 1, whose fragments
+  // every wave waited for (at the top of step kt - 1) before this barrier.
+  // Past the end the last step is fetched again (unused), so every step
+  // leaves NB DMAs in flight and reads a landed stage.  A multiplying wave
+  // issues its NB DMAs between its MFMA groups: issued together after the
+  // barrier, the 8 waves' 32 KiB of DMAs queue in the texture address unit
+  // and hold every wave's MFMAs back by hundreds of cycles.
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no compiler-visible load left in flight
+  auto clampk = [&](int k) { return k < ke ? k : ke - 1; };
   issue(kb, 0);
-  issue(kb + 1 < ke ? kb + 1 : kb, 1);
-  int stg = 0;
-  for (int kt = kb; kt < ke; ++kt) {
-    dma_wait_barrier<NB>();
-    // Step kt + 2 into the stage read at step kt - 1; past the end the last
-    // step is fetched again (unused), so every step leaves NB DMAs in flight.
-    issue(kt + 2 < ke ? kt + 2 : ke - 1, stg == 0 ? 2 : stg - 1);
-    if (active) mma_64x128_dsasm(lds + stg * SW_STAGE, lds + stg * SW_STAGE, lane, 64 * wr, brow, acc);
-    stg = stg == 2 ? 0 : stg + 1;
+  issue(clampk(kb + 1), 1);
+  issue(clampk(kb + 2), 2);
+  dma_wait_barrier<2 * NB>();  // stage kb landed
+  u32x4 fa[4], fb[8], ga[4], gb[8];
+  // Fragment bases in stage 0 (a stage is SW_STAGE * 2 bytes further on).
+  const uint32_t fa0 = frag_64x128_base(lds, lane, 64 * wr), fb0 = frag_64x128_base(lds, lane, brow);
+  constexpr uint32_t SB = SW_STAGE * 2;
+  if (active) {
+    frag_64x128_read<0>(fa0, fb0, fa, fb);
+    frag_64x128_read<1>(fa0, fb0, fa, fb);
+    frag_64x128_read<2>(fa0, fb0, fa, fb);
+    frag_64x128_read<3>(fa0, fb0, fa, fb);
+    frag_64x128_read<4>(fa0, fb0, fa, fb);
+    frag_64x128_read<5>(fa0, fb0, fa, fb);
+    frag_64x128_read<6>(fa0, fb0, fa, fb);
+    frag_64x128_read<7>(fa0, fb0, fa, fb);
+    frag_64x128_read<8>(fa0, fb0, fa, fb);
+    frag_64x128_read<9>(fa0, fb0, fa, fb);
+    frag_64x128_read<10>(fa0, fb0, fa, fb);
+    frag_64x128_read<11>(fa0, fb0, fa, fb);
   }
+  int stg = 0;  // stage of step kt
+  constexpr int GPD = 8 / NB;  // MFMA groups per DMA
+  for (int kt = kb; kt < ke; kt += 2) {
+    dma_wait_barrier<NB>();
+    int kn = clampk(kt + 3), sn = (stg + 3) & 3;
+    stg = (stg + 1) & 3;
+    if (active) {
+      frags_64x128_wait(fa, fb);
+      const uint32_t na = fa0 + stg * SB, nb = fb0 + stg * SB;
+      mma_64x128_frags(fa, fb, acc, [&](auto gc) {
+        constexpr int g = decltype(gc)::value;
+        if constexpr (g < 6) {
+          frag_64x128_read<2 * g>(na, nb, ga, gb);
+          frag_64x128_read<2 * g + 1>(na, nb, ga, gb);
+        }
+        if constexpr (g % GPD == GPD - 1) issue1(kn, sn, g / GPD);
+      });
+    } else {
+      issue(kn, sn);
+    }
+    if (kt + 1 >= ke) break;
+    dma_wait_barrier<NB>();
+    kn = clampk(kt + 4);
+    sn = (stg + 3) & 3;
+    stg = (stg + 1) & 3;
+    if (active) {
+      frags_64x128_wait(ga, gb);
+      const uint32_t na = fa0 + stg * SB, nb = fb0 + stg * SB;
+      mma_64x128_frags(ga, gb, acc, [&](auto gc) {
+        constexpr int g = decltype(gc)::value;
+        if constexpr (g < 6) {
+          frag_64x128_read<2 * g>(na, nb, fa, fb);
+          frag_64x128_read<2 * g + 1>(na, nb, fa, fb);
+        }
+        if constexpr (g % GPD == GPD - 1) issue1(kn, sn, g / GPD);
+      });
+    } else {
+      issue(kn, sn);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the last (unused) fragment reads
   dma_wait_barrier<0>();  // the epilogue reuses the ring
 
   if (KIND == K_READ) {
