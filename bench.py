@@ -41,8 +41,8 @@ SEED = 20260729
 TRAFFIC_PREFILL_C2 = 1049.5e6       # one prefill_mfma_kernel launch
 TRAFFIC_PREFILL_C2_PASS = 1116.8e6  # the whole C2 pass (transpose_v, prefill, ctx)
 TRAFFIC_DECODE_C3 = 428.0e6         # one decode_kernel launch
-TRAFFIC_LONG_C4 = 3567.0e6          # the carry and prefill_mfma launches of one C4 call (row chunk 512)
-TRAFFIC_LONG_C4_CALL = 3695.3e6     # the whole C4 call
+TRAFFIC_LONG_C4 = 2659.0e6          # the carry and snap_wide launches of one C4 call (row chunk 512)
+TRAFFIC_LONG_C4_CALL = 2856.5e6     # the whole C4 call
 
 
 def parse():
@@ -199,9 +199,9 @@ def bench_prefill(torch, args):
 
 
 def bench_long(torch, args):
-    """C4: one long stream per head, T = 8192 (8 state-carry intervals at the
-    automatic row chunk of 1024: the state-carry launch, then one launch of
-    every interval's gram and readout tiles)."""
+    """C4: one long stream per head, T = 8192 (16 state-carry intervals at the
+    automatic row chunk of 512: the state-carry launch, then one launch of
+    every interval's gram and readout tiles, then the context launch)."""
     from burn_dragon_amd import _lib
     B, H, T, N, D, C = 1, 4, 8192, 8192, 256, 256
     dev = torch.device("cuda")
@@ -226,8 +226,8 @@ def bench_long(torch, args):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     # The same call at the config's row chunk of 256 (32 state intervals):
-    # the result is the same up to rounding; the automatic row chunk (1024)
-    # writes a quarter of the state snapshots.
+    # the result is the same up to rounding; the automatic row chunk (512)
+    # writes half as many state snapshots.
     for _ in range(2):
         lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho, chunk=C)
     e0.record()
@@ -252,7 +252,7 @@ def bench_long(torch, args):
             "unit": "tokens/s", "ms_per_prefill": ms, "steps": steps,
             "config": {"workload": "C4 long prefill, one BDH layer: B1 nh4 T8192 N8192 D256, "
                                    "bf16 in / fp32 acc, RoPE fused; automatic row chunk (rho "
-                                   "snapshots every 1024 tokens), credited at the config's "
+                                   "snapshots every 512 tokens), credited at the config's "
                                    f"chunk {C}"},
             "at_config_chunk": {"chunk": C, "ms_per_prefill": round(ms_c, 4),
                                 "tokens_per_s": round(B * T / (ms_c * 1e-3), 1)},

@@ -287,17 +287,16 @@ bdh_status check_plan(const bdh_recurrent_plan* p) {
 // and the carries in between go through the chunk-pair score blocks.  L is
 // the call's row chunk (the reference's dense_score_row_chunk, config.rs:46,
 // default 512 at config.rs:10, used as linear.rs:117-118 uses it), shortened
-// to the call's length rounded up to 128.  Chunk 0 picks 512, or 1024 from
-// 4096 tokens on, where the halved number of state materialisations
-// outweighs the doubled score work (T = 8192, N = 8192, D = 256: 1.13 ms per
-// call against 1.22 ms at 512; 768 is as fast, 256 takes 1.49 ms).
+// to the call's length rounded up to 128.
 constexpr int64_t kMaxRowChunk = 4096;
-// Row chunk 0 = auto: 512, the reference's default, or 1024 from 4096 tokens:
-// with decay (per-interval launch chain) halving the launches pays for the
-// longer score blocks; without decay (state-carry form) half the snapshots
-// do (C4: 0.83 ms at 1024 against 0.875 at 512 and 0.90 at 256).
-int64_t state_interval(int64_t T, int32_t chunk) {
-  const int64_t L = chunk > 0 ? chunk : (T >= 4096 ? 1024 : 512);
+// Row chunk 0 = auto: 512, the reference's default.  With decay (the
+// per-interval launch chain) 1024 from 4096 tokens on: halving the launches
+// pays for the longer score blocks (T = 8192, N = 8192, D = 256: 1.13 ms per
+// call against 1.22 ms at 512).  Without decay (the state-carry form) 512
+// stays faster: the gram work grows with the chunk, the snapshots shrink
+// with it (C4: 0.74 ms at 512, 0.77 at 768, 0.81 at 1024).
+int64_t state_interval(int64_t T, int32_t chunk, bool decay) {
+  const int64_t L = chunk > 0 ? chunk : (decay && T >= 4096 ? 1024 : 512);
   return T < L ? ((T + 127) / 128) * 128 : L;
 }
 
@@ -407,7 +406,7 @@ bdh_status forward_common(const bdh_recurrent_plan* plan, int32_t dtype, const v
   a.T = T;
   a.N = N;
   a.D = D;
-  a.L = want_rho ? state_interval(T, chunk) : ((T + 127) / 128) * 128;
+  a.L = want_rho ? state_interval(T, chunk, decay != nullptr) : ((T + 127) / 128) * 128;
   a.state = want_rho;
   st = run_bf16_path(a, hs, &prof.launches);
   if (st != BDH_OK) return st;
@@ -642,7 +641,7 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
   a.T = p.time;
   a.N = p.latent;
   a.D = p.embd;
-  a.state_interval = state_interval(p.time, 0);
+  a.state_interval = state_interval(p.time, 0, false);  // layer attention has no decay
   st = run_layer(a, (hipStream_t)stream, &prof.launches);
   if (st == BDH_OK) prof.done(true);
   return st;

@@ -173,9 +173,32 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
 
   if (!wave_on) return;
   float* C = a.ctx + (s * a.T + t0) * a.D;
-  const bool rd = a.rd != nullptr && iv >= a.rd_iv0;
-  const float* RD = rd ? a.rd + (s * a.T + t0) * a.D : nullptr;
-  const int64_t rd_stride = a.S * a.T * a.D;
+  if (a.rd != nullptr && iv >= a.rd_iv0) {
+    // Readout partials added in split order, every load of a partial issued
+    // before any context store: loads after a store that the compiler cannot
+    // prove distinct would each wait out a memory round trip.
+    const float* RD = a.rd + (s * a.T + t0) * a.D;
+    const int64_t rd_stride = a.S * a.T * a.D;
+    for (int kp = 0; kp < a.rd_kr; ++kp) {
+      float rv[2][NI][16];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t row = r0 + mi * 32 + acc_row(lane, r);
+            const int64_t d = ecol + ni * 32 + acc_col(lane);
+            rv[mi][ni][r] = row < Lc && d < a.D ? RD[kp * rd_stride + row * a.D + d] : 0.0f;
+          }
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mi][ni][r] += rv[mi][ni][r];
+    }
+  }
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -184,12 +207,7 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int64_t row = r0 + mi * 32 + acc_row(lane, r);
         const int64_t d = ecol + ni * 32 + acc_col(lane);
-        if (row < Lc && d < a.D) {
-          float v = acc[mi][ni][r];
-          if (rd)
-            for (int kp = 0; kp < a.rd_kr; ++kp) v += RD[kp * rd_stride + row * a.D + d];
-          C[row * a.D + d] = v;
-        }
+        if (row < Lc && d < a.D) C[row * a.D + d] = acc[mi][ni][r];
       }
 }
 
