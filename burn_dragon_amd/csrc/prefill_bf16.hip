@@ -481,6 +481,55 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   if (launches) *launches += 4;
   return BDH_OK;
 }
+
+// Context only (no state, no carried state), queries already rotated, no
+// decay: v^T, the gram tiles in 8-wave workgroups (snap_wide.hip, the tiles
+// of the state-carry form without readouts), the context kernel.  N splits:
+// the fewest of 1, 2 or 4 with the fewest steps in rounds of units over the
+// CUs.  (The layer's attention runs here: the layer rotates q in its GEMM
+// epilogue.)
+bdh_status run_gram_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, int64_t S, int64_t Tp,
+                         int64_t Dp, int64_t Lp, int nb, int nk) {
+  const int64_t L = a.L;
+  const int64_t slots = device_cus();
+  const int64_t upg = (int64_t)nb * (nb - 1) / 2 + nb;
+  auto rounds = [&](int k) { return (S * k * upg + slots - 1) / slots * (nk / k); };
+  int ks = 1;
+  for (int cand = 2; cand <= 4 && nk % (2 * cand) == 0; cand *= 2)
+    if (rounds(cand) < rounds(ks)) ks = cand;
+
+  void *vt = nullptr, *part = nullptr;
+  bdh_status stt = scratch(st, SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
+  if (stt != BDH_OK) return stt;
+  stt = scratch(st, SLOT_SCORES, (size_t)(ks * S * Lp * Lp) * sizeof(float), &part);
+  if (stt != BDH_OK) return stt;
+
+  hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, VT_TILE), cdiv(Dp, VT_TILE), (unsigned)(a.B * a.Hv)),
+                     dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
+  BDH_HIP_TRY(hipGetLastError());
+
+  PrefillArgs p{};
+  p.x = a.x;
+  p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;
+  p.part = (float*)part;
+  p.L = L; p.Lp = Lp; p.n_iv = 1;
+  p.ks = ks; p.nb = nb;
+  p.gram_groups = (int)(S * ks);
+  p.rd_pg = 0;
+  p.gram_ids = snap_wide_ids(p.gram_groups, nb, 0);
+  p.vt = (const bf16_t*)vt;
+  p.Tp = Tp; p.Dp = Dp;
+  const int kt = ktime_begin(BDH_KERNEL_PREFILL, st);
+  BDH_HIP_TRY(launch_snap_wide(p, st));
+  ktime_end(kt, st);
+
+  const int64_t Lc0 = a.T < L ? a.T : L;
+  CtxArgs cx{(const bf16_t*)vt, (const float*)part, a.ctx, a.H, a.Hv, a.T, a.D, L, Lp, Tp, Dp, S,
+             1, 0, 1, (int)cdiv(Lc0, CTX_ROWS), nullptr, 0, 0};
+  BDH_HIP_TRY(launch_ctx(cx, ks, st));
+  if (launches) *launches += 3;
+  return BDH_OK;
+}
 }  // namespace
 
 bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) {
@@ -505,6 +554,8 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   if (a.state && n_iv >= 2 && a.decay == nullptr && a.D * a.N * 2 < ((int64_t)1 << 31) &&
       (size_t)(n_iv * S * a.N * a.D) * sizeof(bf16_t) <= kCarrySnapMax)
     return run_carry_path(a, st, launches, S, Tp, Dp, n_iv, Lp, nb, nk);
+  if (!a.state && a.rho_in == nullptr && a.freqs == nullptr && a.decay == nullptr && n_iv == 1)
+    return run_gram_path(a, st, launches, S, Tp, Dp, Lp, nb, nk);
 
   // N splits of the gram: the fewest for which the longest gram unit stays
   // within ~85% of the first launch's average work per workgroup slot (two

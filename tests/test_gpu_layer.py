@@ -26,6 +26,7 @@ def _case(rng, B, H, T, N, D):
     (3, 2, 16, 512, 128, 2, False),     # few-row GEMMs, four 16-row blocks (M = 48)
     (1, 1, 40, 256, 2048, 3, True),     # widest embd: 32 values a lane in the LayerNorms
     (2, 1, 160, 256, 1024, 0, False),   # wide embd on the 256 x 128 tiles (M = 320)
+    (1, 2, 1000, 512, 64, 3, False),    # context only over 4 gram row blocks, the last ragged
 ])
 def test_layer_matches_oracle(oracle, B, H, T, N, D, pos, want_rho):
     torch = need_gpu()

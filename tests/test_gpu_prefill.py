@@ -281,6 +281,26 @@ def test_dense_causal_attention_bf16_and_limits(oracle):
     assert bd.try_fused_dense_causal_attention(qd, vd, torch.ones(3, device="cuda")) is None
 
 
+@pytest.mark.parametrize("B,H,T,N,D", [
+    (1, 2, 1000, 512, 64),    # 4 row blocks, the last ragged (232 rows)
+    (2, 1, 1024, 256, 320),   # whole row blocks, two 256-column context blocks
+])
+def test_dense_causal_attention_bf16_several_tiles(oracle, B, H, T, N, D):
+    # Context only on pre-rotated queries with a decay (ones) given, as the
+    # entry point requires: several gram row blocks, ragged or whole.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(T + N + D)
+    q = oracle.round_bf16(oracle.rope_rotate(rc.sparse_relu(rng, (B, H, T, N))))
+    v = oracle.round_bf16(rc.gaussian(rng, (B, 1, T, D), 1 / 16))
+    announce("dense bf16", B, H, T, N, D)
+    out = bd.try_fused_dense_causal_attention(dev(torch, q, torch.bfloat16),
+                                              dev(torch, v, torch.bfloat16), dev(torch, np.ones(H, np.float32)))
+    torch.cuda.synchronize()
+    cref, _ = oracle.dense_score_f64(q, v, None, None, want_rho=False)
+    assert rel_l2(host(out), cref) <= TOL_BF16
+
+
 @pytest.mark.parametrize("decay", [[0.0, 0.9], [-0.9, 0.5], [-0.5, 0.0]])
 def test_bf16_decay_zero_and_negative(oracle, decay):
     # Decay powers d^e as repeated products give them (recurrent.rs:415):
