@@ -203,7 +203,8 @@ int prefill_carry_units(int64_t S, int64_t N, int64_t Dp);
 // Gram and readout tiles of the state-carry form in 8-wave workgroups
 // (snap_wide.hip): PrefillArgs in snapshot mode (rd_snap, rd_iv0, rd_pg =
 // readout tiles per group = 256-row blocks x 256-column blocks, rd_kr = ks),
-// gram_ids = snap_wide_ids(groups, nb, rd_pg).
+// gram_ids = snap_wide_ids(groups, nb, rd_pg).  With rd_pg = 0 (no readout
+// tiles) it is the gram of a context-only call on pre-rotated queries.
 int snap_wide_ids(int groups, int nb, int rd_pg);
 hipError_t launch_snap_wide(const PrefillArgs& a, hipStream_t st);
 hipError_t launch_prefill_carry(const CarryArgs& a, hipStream_t st);
