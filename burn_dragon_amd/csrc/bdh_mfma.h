@@ -161,6 +161,16 @@ __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t
                "{m0}"(m0)
                : "memory");
 }
+// As dma16 with 4 bytes per lane, written to LDS at m0 + 4 * lane.
+__device__ __forceinline__ void dma4(const void* gbase, uint32_t voff, uint32_t m0) {
+  const uint64_t b = reinterpret_cast<uint64_t>(gbase);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t bu = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(reinterpret_cast<const void*>(bu)),
+               "{m0}"(m0)
+               : "memory");
+}
 // Wait until at most N of this wave's vector memory operations are in
 // flight (the oldest complete first), then a workgroup barrier: every wave's
 // DMAs issued before its last N have landed in LDS, and every wave has

@@ -20,8 +20,9 @@
 //
 // q = RoPE(x) is applied between HBM and LDS: each lane computes the packed
 // bf16 (cos, sin) words of its 4 pairs from the f32 phase frac(p f) (v_cos /
-// v_sin take revolutions) and rotates with v_dot2.  K steps are 32 deep; LDS holds two steps (double buffer) and the
-// global loads of step k+1 are in flight while step k is multiplied.  Every
+// v_sin take revolutions) and rotates with v_dot2.  K steps are 32 deep; LDS
+// holds two steps (double buffer) and the loads of later steps are in flight
+// while step k is multiplied (the RoPE gram tiles' x two steps ahead).  Every
 // unit runs an even number of steps (the host guarantees it), so the step
 // loop has a single exit; with a mid-loop exit the compiler moves the
 // accumulators between AGPRs and VGPRs on every iteration.
@@ -152,23 +153,52 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
     }
     dma_wait_barrier<0>();  // the epilogue reuses the ring
   } else {
-    // RoPE: x and the step's frequencies one step ahead in registers; each
-    // thread rotates its chunks (phases computed per row) as it writes them
-    // to LDS.  (Rotating in place in a direct-load ring was slower: the
-    // rotation's VALU work, not the loads, bounds these steps.)
+    // RoPE: each lane's raw x chunks and the step's frequencies arrive by
+    // direct loads two steps ahead in lane-private LDS slots (the third
+    // buffer; the frequencies after it).  At the top of a step the lane reads
+    // the next step's slots into registers and refills them with the step
+    // after; after the MFMAs it rotates what it read into the other operand
+    // buffer.  The loads then have a whole step to land, where loads into
+    // registers one step ahead had only the MFMA phase (C2: 258 -> 253 us).
+    // A lane reads back only what its own loads wrote (wave w's load of group
+    // g fills rows 64 g + 16 w + l/4, chunk l & 3 for lane l: that lane's
+    // (rb, kc)), so the slots need waits but no barrier.  (Rotating each
+    // group between the MFMA groups instead was slower: 266 us.)
     struct Stage {
       uint4 xr[6];
       float fq[4];
     } st;
-    auto load = [&](int kt) {
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+    const uint32_t raw0 = lds0 + (uint32_t)(2 * BUF * 2);
+    const uint32_t fq0 = lds0 + (uint32_t)(3 * BUF * 2 + w * 256);
+    const char* rawp = reinterpret_cast<const char*>(lds + 2 * BUF) + w * 1024 + 16 * lane;
+    const float* fqp = reinterpret_cast<const float*>(lds + 3 * BUF) + w * 64 + 4 * kc;
+    // Step kt's x chunks, then its 16 pair frequencies (lane l: the even
+    // neuron 32 kt + 2 (l & 15); lanes 4 kc .. 4 kc + 3 are this lane's).
+    auto issue = [&](int kt) {
 #pragma unroll
       for (int g = 0; g < 6; ++g) {
         if (g >= groups) break;
         uint32_t off;
         const int64_t o = at(g, kt, off);
-        st.xr[g] = ldg16_off(X + o, off);
+        dma16(X + o, off, raw0 + (uint32_t)((g * 4 + w) * 1024));
       }
-      load_freq4(a.freqs + (int64_t)kt * BK + kc * 8, st.fq);
+      dma4(a.freqs + (int64_t)kt * BK, (uint32_t)(8 * (lane & 15)), fq0);
+    };
+    // The slots into registers; they may be refilled once this returns.
+    auto pull = [&]() {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int g = 0; g < 6; ++g) {
+        if (g >= groups) break;
+        st.xr[g] = *reinterpret_cast<const uint4*>(rawp + g * 4096);
+      }
+      const float4 f = *reinterpret_cast<const float4*>(fqp);
+      st.fq[0] = f.x;
+      st.fq[1] = f.y;
+      st.fq[2] = f.z;
+      st.fq[3] = f.w;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
     auto store = [&](int buf) {
       bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
@@ -181,7 +211,28 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
     auto compute = [&](int buf) {
       if (active) mma_64x128(lds + buf * BUF, lds + buf * BUF, lane, 64 * w, brow, acc);
     };
-    run_steps(kb, ke, load, store, compute);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no compiler-visible load left in flight
+    auto clampk = [&](int k) { return k < ke ? k : ke - 1; };
+    issue(kb);
+    pull();
+    issue(clampk(kb + 1));
+    store(0);
+    __syncthreads();
+    // Past the end the last step is fetched again (unused).
+    for (int kt = kb; kt < ke; kt += 2) {
+      pull();  // step kt + 1 (ke - kb is even)
+      issue(clampk(kt + 2));
+      compute(0);
+      store(1);
+      __syncthreads();
+      pull();  // step kt + 2
+      issue(clampk(kt + 3));
+      compute(1);
+      if (kt + 2 < ke) store(0);
+      __syncthreads();
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unused loads, before the epilogue reuses LDS
+    __syncthreads();
   }
 
   // Scores of rows ti < Lc and columns tj < Lc: times d^(ti - tj) below
@@ -482,8 +533,10 @@ __device__ __forceinline__ void tile_of(int u, int& rbk, int& cbk) {
 
 template <bool ROPE, bool DECAY>
 __global__ __launch_bounds__(NT, 2) void prefill_mfma_kernel(PrefillArgs a) {
-  // Two register-path buffers, or the three-stage ring of the direct-load gram.
-  __shared__ __attribute__((aligned(16))) bf16_t lds[3 * BUF];
+  // Three operand buffers (the direct-load ring of the gram without RoPE; with
+  // RoPE two operand buffers and the lane-private x slots), then the RoPE
+  // gram's frequency slots (256 bytes a wave).
+  __shared__ __attribute__((aligned(16))) bf16_t lds[3 * BUF + 512];
   const int id = blockIdx.x;
   if (id < a.gram_ids) {
     const int tpg = units_per_group(a.nb);
