@@ -20,7 +20,8 @@
 //
 // q = RoPE(x) is applied between HBM and LDS: each lane computes the packed
 // bf16 (cos, sin) words of its 4 pairs from the f32 phase frac(p f) (v_cos /
-// v_sin take revolutions) and rotates with v_dot2.  K steps are 32 deep; LDS
+// v_sin take revolutions; the gram tiles advance it from one row group to the
+// next by a complex multiply) and rotates with v_dot2.  K steps are 32 deep; LDS
 // holds two steps (double buffer) and the loads of later steps are in flight
 // while step k is multiplied (the RoPE gram tiles' x two steps ahead).  Every
 // unit runs an even number of steps (the host guarantees it), so the step
@@ -200,12 +201,55 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
       st.fq[3] = f.w;
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
+    // Packed (cos, sin) words of each group's row for the step in st,
+    // computed before the MFMAs of the current step (the rotation itself
+    // follows them).  A lane's rows in groups g and g + 1 of one operand lie
+    // 64 tokens apart (0 with fixed positions), so only the first group of
+    // each operand takes its phase from frac(p f) and two transcendentals;
+    // the others advance it by one complex multiply with e(64 f).  (C2: 253 ->
+    // 249 us; the advance alone, after the MFMAs, gained nothing.)  Rows past
+    // a ragged interval take advanced phases instead of their clamped row's:
+    // their scores are never stored.
+    uint4 csw[6];
+    auto phases = [&]() {
+      float c[4], sn[4], ec[4], es[4];
+      const float dstep = a.fixed ? 0.0f : 64.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float fe = rope_frac(dstep, st.fq[j]);
+        ec[j] = __builtin_amdgcn_cosf(fe);
+        es[j] = __builtin_amdgcn_sinf(fe);
+      }
+      constexpr int anchor2 = PAIR ? 2 : 4;
+#pragma unroll
+      for (int g = 0; g < 6; ++g) {
+        if (g >= groups) break;
+        if (g == 0 || g == anchor2) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float fr = rope_frac(pg[g], st.fq[j]);
+            c[j] = __builtin_amdgcn_cosf(fr);
+            sn[j] = __builtin_amdgcn_sinf(fr);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float nc = c[j] * ec[j] - sn[j] * es[j];
+            const float ns = sn[j] * ec[j] + c[j] * es[j];
+            c[j] = nc;
+            sn[j] = ns;
+          }
+        }
+        csw[g] = make_uint4(pack_bf16x2(c[0], sn[0]), pack_bf16x2(c[1], sn[1]), pack_bf16x2(c[2], sn[2]),
+                            pack_bf16x2(c[3], sn[3]));
+      }
+    };
     auto store = [&](int buf) {
       bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
 #pragma unroll
       for (int g = 0; g < 6; ++g) {
         if (g >= groups) break;
-        *reinterpret_cast<uint4*>(&base[lds_off(64 * g + rb, kc)]) = rot8_bf16(st.xr[g], rope_cs4(pg[g], st.fq));
+        *reinterpret_cast<uint4*>(&base[lds_off(64 * g + rb, kc)]) = rot8_bf16(st.xr[g], csw[g]);
       }
     };
     auto compute = [&](int buf) {
@@ -216,17 +260,20 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
     issue(kb);
     pull();
     issue(clampk(kb + 1));
+    phases();
     store(0);
     __syncthreads();
     // Past the end the last step is fetched again (unused).
     for (int kt = kb; kt < ke; kt += 2) {
       pull();  // step kt + 1 (ke - kb is even)
       issue(clampk(kt + 2));
+      phases();
       compute(0);
       store(1);
       __syncthreads();
       pull();  // step kt + 2
       issue(clampk(kt + 3));
+      phases();
       compute(1);
       if (kt + 2 < ke) store(0);
       __syncthreads();
