@@ -6,7 +6,7 @@ from .recurrent import (CompiledRecurrentAttentionPlan, KernelProfileSnapshot,  
                         RecurrentAttentionOutput, RecurrentProfileSnapshot, alibi_decay,
                         default_alibi_slopes,
                         recurrent_profile_enable, recurrent_profile_reset,
-                        recurrent_profile_snapshot, supports_backend,
+                        recurrent_profile_snapshot, release_stream_scratch, supports_backend,
                         supports_recurrent_backend, try_fused_recurrent_attention,
                         try_fused_recurrent_attention_rope,
                         try_fused_recurrent_attention_wgpu,

@@ -72,7 +72,20 @@ bdh_status scratch(hipStream_t st, int slot, size_t bytes, void** out, bool zero
   stream_capturing(st, &capturing);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   ScratchSet& ss = g_sets[{dev, st}];
-  if (capturing) ss.captured = true;
+  if (capturing) {
+    ss.captured = true;
+  } else if (ss.captured) {
+    // The first eager call after a capture leaves the set's buffers to the
+    // captured graphs (retired: kept until bdh_scratch_release) and takes
+    // fresh ones, so a replay on another stream never shares a buffer with
+    // eager work on the capturing stream.
+    for (int i = 0; i < SLOT_COUNT; ++i) {
+      if (ss.ptr[i]) ss.retired.push_back(ss.ptr[i]);
+      ss.ptr[i] = nullptr;
+      ss.bytes[i] = 0;
+    }
+    ss.captured = false;
+  }
   if (bytes == 0) bytes = 256;
   if (ss.bytes[slot] < bytes) {
     if (capturing)

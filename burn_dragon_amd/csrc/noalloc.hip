@@ -2,10 +2,13 @@
 // device allocation, for callers that cannot allocate (code under HIP graph
 // capture, tight serving loops).  Its buffers live in one file-scope device
 // array of NOALLOC_BYTES, one copy per GPU, shared by every call on that GPU
-// (calls that overlap on one GPU race on it):
-//   [0, FREQ_BYTES)   RoPE frequency table of the last (latent, theta) used
-//                     on the device, uploaded from the host when it changes;
-//   [FREQ_BYTES, ..)  range readouts, range lists and counts of a stream
+// (calls that overlap on one GPU race on its range region):
+//   [0, TABLE_BYTES)  RoPE frequency tables, one slot per (latent, theta)
+//                     used on the device, assigned in order of first use and
+//                     never overwritten: a graph captured with one key keeps
+//                     valid frequencies whatever keys later calls use.  A key
+//                     that no longer fits is refused (BDH_UNSUPPORTED);
+//   [TABLE_BYTES, ..) range readouts, range lists and counts of a stream
 //                     split into row ranges (decode_part_bytes), every
 //                     element written by the decode kernel before the
 //                     finalize kernel reads it, so nothing needs clearing.
@@ -14,6 +17,7 @@
 // device and is kept per device.
 #include <string.h>
 
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -22,21 +26,30 @@
 namespace {
 
 constexpr size_t NOALLOC_BYTES = (size_t)16 << 20;
-constexpr int64_t NOALLOC_MAX_LATENT = (int64_t)1 << 20;
-constexpr size_t FREQ_BYTES = (size_t)NOALLOC_MAX_LATENT * sizeof(float);  // 4 MiB
+constexpr size_t TABLE_BYTES = (size_t)8 << 20;
+constexpr size_t RANGE_BYTES = NOALLOC_BYTES - TABLE_BYTES;
+constexpr int64_t NOALLOC_MAX_LATENT = (int64_t)1 << 20;  // one table of 4 MiB
 
 static __device__ __align__(256) unsigned char noalloc_scratch[NOALLOC_BYTES];
+
+struct TableSlot {
+  int64_t latent;
+  uint32_t theta_bits;
+  size_t offset;                     // from the start of the array
+  std::unique_ptr<float[]> host;     // host copy; outlives its upload
+};
 
 constexpr int kMaxDevices = 64;
 struct DeviceSlot {
   bool ready = false;
   unsigned char* ptr = nullptr;  // this device's copy of noalloc_scratch
-  int64_t latent = 0;            // key of the table held in the array
-  uint32_t theta_bits = 0;
-  std::vector<float> host;       // host copy of that table
+  size_t table_used = 0;         // bytes of the table region assigned
+  std::vector<TableSlot> tables;
 };
 std::mutex g_mu;
 DeviceSlot g_dev[kMaxDevices];
+
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
 }  // namespace
 
@@ -63,7 +76,7 @@ extern "C" bdh_status bdh_decode_step_noalloc(int64_t batch, int64_t heads, int6
     return fail(BDH_UNSUPPORTED, "position must lie in [0, 2^24)");
   if (rope && !(rope->theta > 0.0f)) return fail(BDH_EINVAL, "rope theta must be > 0");
   if (latent > NOALLOC_MAX_LATENT)
-    return fail(BDH_UNSUPPORTED, "bdh_decode_step_noalloc: latent exceeds 1048576 (its frequency table region)");
+    return fail(BDH_UNSUPPORTED, "bdh_decode_step_noalloc: latent exceeds 1048576 (one frequency table slot)");
 
   hipStream_t st = (hipStream_t)stream;
   DecodeArgs a;
@@ -83,10 +96,10 @@ extern "C" bdh_status bdh_decode_step_noalloc(int64_t batch, int64_t heads, int6
   a.N = latent;
   a.D = embd;
   const size_t part = decode_part_bytes(a);
-  if (part > NOALLOC_BYTES - FREQ_BYTES)
+  if (part > RANGE_BYTES)
     return fail(BDH_UNSUPPORTED, "bdh_decode_step_noalloc: the range buffers of this shape exceed its " +
-                                     std::to_string((NOALLOC_BYTES - FREQ_BYTES) >> 20) +
-                                     " MiB scratch array; use bdh_decode_step");
+                                     std::to_string(RANGE_BYTES >> 20) +
+                                     " MiB range region; use bdh_decode_step");
 
   int dev = 0;
   BDH_HIP_TRY(hipGetDevice(&dev));
@@ -104,9 +117,19 @@ extern "C" bdh_status bdh_decode_step_noalloc(int64_t batch, int64_t heads, int6
   if (rope) {
     uint32_t tb;
     memcpy(&tb, &rope->theta, 4);
-    if (ds.latent != latent || ds.theta_bits != tb) {
-      // A new table: computed on the host (attention.rs:552-576, the same
-      // f32 arithmetic as every other entry point), copied into the array.
+    const TableSlot* slot = nullptr;
+    for (const TableSlot& t : ds.tables)
+      if (t.latent == latent && t.theta_bits == tb) slot = &t;
+    if (!slot) {
+      // A new key gets the next free slot, computed on the host
+      // (attention.rs:552-576, the same f32 arithmetic as every other entry
+      // point) and copied in.  Slots already assigned are never touched.
+      const size_t bytes = round256((size_t)latent * sizeof(float));
+      if (ds.table_used + bytes > TABLE_BYTES)
+        return fail(BDH_UNSUPPORTED,
+                    "bdh_decode_step_noalloc: its " + std::to_string(TABLE_BYTES >> 20) +
+                        " MiB frequency-table region holds " + std::to_string(ds.tables.size()) +
+                        " (latent, theta) keys and has no room for another; use bdh_decode_step");
       bool capturing = false;
       stream_capturing(st, &capturing);
       if (capturing)
@@ -114,18 +137,24 @@ extern "C" bdh_status bdh_decode_step_noalloc(int64_t batch, int64_t heads, int6
                     "bdh_decode_step_noalloc: the RoPE table of this (latent, theta) is uploaded on "
                     "its first call on the device, which cannot happen during graph capture: call "
                     "it once eagerly first");
-      ds.host.resize((size_t)latent);
-      rope_freqs_host(latent, rope->theta, ds.host.data());
-      BDH_HIP_TRY(hipMemcpyAsync(ds.ptr, ds.host.data(), (size_t)latent * sizeof(float),
+      TableSlot t;
+      t.latent = latent;
+      t.theta_bits = tb;
+      t.offset = ds.table_used;
+      t.host.reset(new float[(size_t)latent]);
+      rope_freqs_host(latent, rope->theta, t.host.get());
+      BDH_HIP_TRY(hipMemcpyAsync(ds.ptr + t.offset, t.host.get(), (size_t)latent * sizeof(float),
                                  hipMemcpyHostToDevice, st));
-      // The host copy must outlive the transfer.
+      // Later calls may run on other streams: the table is complete before
+      // this call returns.
       BDH_HIP_TRY(hipStreamSynchronize(st));
-      ds.latent = latent;
-      ds.theta_bits = tb;
+      ds.table_used += bytes;
+      ds.tables.push_back(std::move(t));
+      slot = &ds.tables.back();
     }
-    a.freqs = (const float*)ds.ptr;
+    a.freqs = (const float*)(ds.ptr + slot->offset);
   }
-  a.part_buf = ds.ptr + FREQ_BYTES;
-  a.part_bytes = NOALLOC_BYTES - FREQ_BYTES;
+  a.part_buf = ds.ptr + TABLE_BYTES;
+  a.part_bytes = RANGE_BYTES;
   return run_decode(a, st, nullptr);
 }

@@ -249,6 +249,25 @@ bdh_status bdh_state_record_load(const char* path, int32_t n_layers, const bdh_l
   Pinned pin;
   s = pin.init();
   if (s != BDH_OK) return s;
+  // First pass, host only: every layer's block is read and its checksum
+  // checked before any device memory is written, so a corrupt or truncated
+  // record leaves the caller's state as it was (as a failed restore of the
+  // reference leaves the model untouched, runtime_checkpoint.rs:163-200).
+  for (int32_t i = 0; i < n_layers; ++i) {
+    const Entry& e = ent[i];
+    if (!e.bytes) continue;
+    if (fseek(file.f, (long)e.offset, SEEK_SET) != 0) return fail(BDH_EINVAL, "seek failed");
+    uint32_t crc = kCrcInit;
+    for (int64_t lo = 0; lo < e.bytes; lo += (int64_t)kChunk) {
+      const size_t len = (size_t)(e.bytes - lo) < kChunk ? (size_t)(e.bytes - lo) : kChunk;
+      if (fread(pin.p[0], 1, len, file.f) != len) return fail(BDH_EINVAL, "truncated rho block");
+      crc = crc32c_update(crc, (const unsigned char*)pin.p[0], len);
+    }
+    if (crc32c_final(crc) != e.crc)
+      return fail(BDH_EINVAL, "layer " + std::to_string(i) + ": rho checksum mismatch (corrupt record)");
+  }
+  // Second pass: the copies, checked again (a file changed between the two
+  // passes is still reported, but then after its copy).
   for (int32_t i = 0; i < n_layers; ++i) {
     const Entry& e = ent[i];
     if (!e.bytes) continue;
@@ -268,7 +287,8 @@ bdh_status bdh_state_record_load(const char* path, int32_t n_layers, const bdh_l
     }
     BDH_HIP_TRY(hipStreamSynchronize(st));
     if (crc32c_final(crc) != e.crc)
-      return fail(BDH_EINVAL, "layer " + std::to_string(i) + ": rho checksum mismatch (corrupt record)");
+      return fail(BDH_EINVAL, "layer " + std::to_string(i) +
+                                  ": rho checksum mismatch (the record changed during the load)");
   }
   return BDH_OK;
 }

@@ -239,3 +239,16 @@ def recurrent_profile_snapshot() -> KernelProfileSnapshot:
     s = _lib.BdhProfileSnapshot()
     _lib.load().bdh_profile_get(ctypes.byref(s))
     return KernelProfileSnapshot(*[getattr(s, f) for f, _ in s._fields_])
+
+
+def release_stream_scratch(stream: "torch.cuda.Stream | None" = None) -> None:
+    """Frees the scratch the library keeps for `stream` (default: the current
+    stream) on the current device, after the stream's queued work.  Call it
+    before a stream is dropped, and only after every graph captured on it that
+    calls this library has been destroyed: the sets are GB-scale at long
+    shapes.  No counterpart in the reference (Burn's allocator owns its
+    buffers)."""
+    s = stream if stream is not None else torch.cuda.current_stream()
+    st = _lib.load().bdh_scratch_release(ctypes.c_void_p(s.cuda_stream))
+    if st != _lib.BDH_OK:
+        raise _lib.BdhError(f"bdh_scratch_release: {_lib.last_error()}")

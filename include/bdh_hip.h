@@ -17,7 +17,14 @@
  *     shape on that stream.  Growth is refused (BDH_UNSUPPORTED) while the
  *     stream is being captured into a graph: run the largest shape once
  *     eagerly on the capturing stream first.  A buffer a captured graph may
- *     still use is never freed before bdh_scratch_release;
+ *     still use is never freed before bdh_scratch_release, and the first
+ *     eager call on a stream after a capture on it takes fresh buffers, so a
+ *     replay (on any stream) never shares scratch with eager work.  Graphs
+ *     captured on one stream share that stream's buffers: their replays
+ *     must not overlap each other.  A stream's scratch (GB-scale at long
+ *     shapes) lives until bdh_scratch_release(stream): call it before a
+ *     stream is destroyed, or a later stream given the same handle inherits
+ *     the set;
  *   - errors are status codes, never aborts.  BDH_UNSUPPORTED is the
  *     reference's `None` ("use the Burn-op reference instead");
  *     bdh_last_error() gives the message (thread-local).
@@ -144,13 +151,16 @@ bdh_status bdh_decode_step(int64_t batch, int64_t heads, int64_t value_heads,
  * reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments and results as bdh_decode_step; its buffers (the RoPE frequency
- * table and the row-range readouts and lists) live in one 16 MiB device
+ * tables and the row-range readouts and lists) live in one 16 MiB device
  * array per GPU, kept until the process ends.  Limits: latent <= 2^20, and
- * the range buffers of the shape within 12 MiB (BDH_UNSUPPORTED beyond,
+ * the range buffers of the shape within 8 MiB (BDH_UNSUPPORTED beyond,
  * with the reason in bdh_last_error).  Every call on a GPU shares that
- * GPU's array, so calls that overlap on one GPU (different streams or
- * threads) race.  The first call with a new (latent, theta) uploads the
- * frequency table (synchronously on `stream`; refused during capture). */
+ * GPU's range buffers, so calls that overlap on one GPU (different streams
+ * or threads) race.  The first call with a new (latent, theta) uploads its
+ * frequency table into a slot of an 8 MiB table region (synchronously on
+ * `stream`; refused during capture); slots are never overwritten, so a
+ * graph captured at one key stays valid after calls at other keys, and a
+ * key that no longer fits the region is refused. */
 bdh_status bdh_decode_step_noalloc(int64_t batch, int64_t heads, int64_t value_heads,
                                    int64_t latent, int64_t embd, const float* x,
                                    const float* value, float* rho, const float* decay,
@@ -272,9 +282,11 @@ bdh_status bdh_lm_logits(const float* hidden, int64_t rows, int64_t embd,
  * `stream` through pinned staging buffers (device-to-host overlapped with
  * the file write); both calls return once the file / the device buffers are
  * complete.  load rejects a record whose layer count or shapes differ from
- * `layers` (BDH_EINVAL) and verifies every checksum after its copy (on a
- * mismatch the layer's buffer holds the corrupt data and BDH_EINVAL is
- * returned).  info reads the header only, so the caller can allocate. */
+ * `layers` (BDH_EINVAL), and verifies every layer's checksum from the file
+ * before it writes any device memory: a corrupt or truncated record returns
+ * BDH_EINVAL with every rho buffer unchanged.  (A file rewritten while the
+ * load runs is still reported, but after its copy.)  info reads the header
+ * only, so the caller can allocate. */
 typedef struct {
   int64_t batch, heads, latent, embd;
   int32_t persist_sequence_state, retain_terminal_sequence_state;

@@ -268,6 +268,16 @@ pub fn save_streaming_state<B: HipHandles>(path: &str, position: usize,
     if st == ffi::BDH_OK { Ok(()) } else { Err(last_error()) }
 }
 
+/// Frees the scratch the library keeps for a backend stream, after that
+/// stream's queued work (bdh_scratch_release).  Call it before the stream is
+/// destroyed and after every graph captured on it is dropped: the library
+/// keeps GB-scale scratch per stream until then.  No counterpart in the
+/// reference (Burn's allocator owns its buffers).
+pub fn release_stream_scratch<B: HipHandles>(device: &B::Device) -> Result<(), String> {
+    let st = unsafe { ffi::bdh_scratch_release(B::hip_stream(device)) };
+    if st == ffi::BDH_OK { Ok(()) } else { Err(last_error()) }
+}
+
 /// The thread-local message of the last failed call.
 pub fn last_error() -> String {
     unsafe {

@@ -72,3 +72,39 @@ def test_python_written_record_loads_and_corruption_is_caught(tmp_path):
     bad.write_bytes(bytes(blob))
     with pytest.raises(_lib.BdhError, match="checksum"):
         bd.load_model_state(bad, torch.device("cuda"))
+
+
+def test_failed_load_leaves_the_destination_unchanged(tmp_path):
+    # A checksum failure in the last layer is found before any layer is
+    # copied: the caller's rho buffers keep their contents.
+    import ctypes
+    torch = need_gpu()
+    from burn_dragon_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(33)
+    shapes = [(2, 2, 64, 32), (1, 2, 128, 16), (2, 1, 32, 64)]
+    rec = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+    path = tmp_path / "three.bdh"
+    staterec.write_record(path, 5, [(r, 1, 0) for r in rec])
+    blob = bytearray(path.read_bytes())
+    blob[-16] ^= 0x01  # inside the last layer's block
+    bad = tmp_path / "bad_last.bdh"
+    bad.write_bytes(bytes(blob))
+    descs = (_lib.BdhLayerStateDesc * 3)()
+    for i, s in enumerate(shapes):
+        descs[i].batch, descs[i].heads, descs[i].latent, descs[i].embd = s
+        descs[i].persist_sequence_state, descs[i].retain_terminal_sequence_state = 1, 0
+    live = [dev(torch, rng.standard_normal(s).astype(np.float32)) for s in shapes]
+    before = [t.clone() for t in live]
+    ptrs = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in live])
+    announce("state record failed load")
+    st = lib.bdh_state_record_load(str(bad).encode(), 3, descs, ptrs, None)
+    torch.cuda.synchronize()
+    assert st == _lib.BDH_EINVAL and "checksum" in _lib.last_error()
+    for a, b in zip(live, before):
+        assert torch.equal(a, b)
+    # the intact record loads into the same buffers
+    assert lib.bdh_state_record_load(str(path).encode(), 3, descs, ptrs, None) == _lib.BDH_OK
+    torch.cuda.synchronize()
+    for t, r in zip(live, rec):
+        assert np.array_equal(host(t), r)

@@ -65,3 +65,53 @@ def test_capture_without_warm_scratch_is_refused():
     assert "capture" in _lib.last_error()
     del graph
     torch.cuda.synchronize()
+
+
+def test_replay_on_another_stream_overlaps_eager_work_on_the_capture_stream(oracle):
+    # A graph captured on stream A is replayed on stream B while an eager call
+    # of the same shape runs on A, with no synchronisation between the two:
+    # the eager call takes fresh scratch (the captured set belongs to the
+    # graph), so both results are exact.
+    import numpy as np
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    from tests.gpu_util import TOL_BF16, dev, host, rel_l2
+    rng = np.random.default_rng(41)
+    B, H, T, N, D = 4, 4, 512, 2048, 128
+
+    def inputs():
+        x = oracle.round_bf16(np.maximum(rng.standard_normal((B, H, T, N), dtype=np.float32) - 1.645,
+                                         0))
+        v = oracle.round_bf16(rng.standard_normal((B, 1, T, D), dtype=np.float32) / 16)
+        return x, v
+
+    (xa, va), (xb, vb) = inputs(), inputs()
+    ta, tva = dev(torch, xa, torch.bfloat16), dev(torch, va, torch.bfloat16)
+    tb, tvb = dev(torch, xb, torch.bfloat16), dev(torch, vb, torch.bfloat16)
+    announce("graph replay on B, eager on A", B, H, T, N, D)
+    ref_a = bd.try_fused_recurrent_attention_rope(ta, tva, position=11)
+    ref_b = bd.try_fused_recurrent_attention_rope(tb, tvb, position=5)
+    stream_a, stream_b = torch.cuda.Stream(), torch.cuda.Stream()
+    stream_a.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream_a):
+        bd.try_fused_recurrent_attention_rope(tb, tvb, position=5)  # warms A's scratch
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream_a):
+        out = bd.try_fused_recurrent_attention_rope(tb, tvb, position=5)
+    assert out is not None
+    torch.cuda.synchronize()
+    for i in range(3):
+        with torch.cuda.stream(stream_a):
+            eager = bd.try_fused_recurrent_attention_rope(ta, tva, position=11)
+        with torch.cuda.stream(stream_b):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert eager is not None
+        assert torch.equal(eager.context, ref_a.context) and torch.equal(eager.rho, ref_a.rho), i
+        assert torch.equal(out.context, ref_b.context) and torch.equal(out.rho, ref_b.rho), i
+    # and the exact results match the oracle
+    for x, v, pos, r in ((xa, va, 11, ref_a), (xb, vb, 5, ref_b)):
+        c_ref, rho_ref = oracle.recurrent_f64(oracle.rope_rotate(x, pos0=pos), v)
+        assert rel_l2(host(r.context), c_ref) <= TOL_BF16
+        assert rel_l2(host(r.rho), rho_ref) <= TOL_BF16
