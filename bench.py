@@ -57,12 +57,14 @@ def parse():
     ap.add_argument("--model-decode-steps", type=int, default=32,
                     help="timed C5 greedy decode steps")
     ap.add_argument("--only", choices=("all", "prefill", "decode", "long", "model", "model-decode",
-                                       "f32", "copy", "rmw"),
+                                       "f32", "copy", "rmw", "ceilings"),
                     default="all",
                     help="one leg only; 'copy' times a 1 GiB device copy (the calibration kernel "
-                         "of the FETCH_SIZE / WRITE_SIZE counter runs); 'rmw' measures the HBM "
-                         "ceilings (read, copy, in-place RMW, RMW of random 1 KiB rows) on a "
-                         "buffer the size of C3's rho")
+                         "of the FETCH_SIZE / WRITE_SIZE counter runs); 'ceilings' (or 'rmw') "
+                         "measures what the device sustains: HBM read, copy, in-place RMW and "
+                         "RMW of random 1 KiB rows on a buffer the size of C3's rho, torch "
+                         "copy_/add_, the bf16 MFMA rate on register operands, and hipBLASLt on "
+                         "the C2 gram and state shapes")
     ap.add_argument("--long-steps", type=int, default=10, help="timed C4 prefills")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="target CPU-baseline wall time (split between prefill and decode)")
@@ -651,51 +653,95 @@ def bench_f32(torch, args):
             "dtype": "f32", **out}
 
 
-def bench_rmw(torch):
-    """HBM ceilings on a 2 GiB buffer (C3's rho: 64 x 4 x 8192 rows of 1 KiB):
-    a read, a copy, an in-place read-modify-write, and a read-modify-write of
-    5 % / 10 % of the 1 KiB rows picked at random (sorted, as a decode step
-    walks each stream's active rows), through bdh_calib_hbm.  Bytes moved: read
-    = size, copy and RMW = 2 x size, row RMW = 2 x rows x 1 KiB."""
+def bench_ceilings(torch):
+    """What this device sustains, measured in the same run as the kernels it
+    bounds:
+      hbm       bdh_calib_hbm on a 2 GiB buffer (C3's rho: 64 x 4 x 8192 rows
+                of 1 KiB): a read, a copy, an in-place read-modify-write, and a
+                read-modify-write of 5 % / 10 % of the 1 KiB rows picked at
+                random (sorted, as a decode step walks each stream's active
+                rows; non-temporal stores, as the step's); beside them torch's
+                copy_ and in-place add_ on the same buffer.  Bytes moved: read
+                = size, copy and RMW = 2 x size, row RMW = 2 x rows x 1 KiB;
+      mfma      bdh_calib_mfma: v_mfma_f32_16x16x32_bf16 and
+                v_mfma_f32_32x32x16_bf16 on register operands, every CU;
+      hipblaslt torch.bmm in bf16 (hipBLASLt) on the C2 gram shape (32 x
+                [512 x 8192] . [8192 x 512], the full square) and the C2 state
+                shape (32 x [8192 x 512] . [512 x 256])."""
     import numpy as np
     from burn_dragon_amd import _lib
     lib = _lib.load()
-    nbytes = 64 * 4 * 8192 * 1024
-    a = torch.zeros(nbytes // 4, device="cuda", dtype=torch.float32)
-    b = torch.empty_like(a)
-    sink = torch.zeros(4, device="cuda", dtype=torch.float32)
-    total_rows = nbytes // 1024
-    rng = np.random.default_rng(SEED + 9)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    out = {"buffer_bytes": nbytes}
 
-    def run(name, kind, buf2, rows, moved):
-        n_rows = 0 if rows is None else rows.numel()
-        call = lambda: lib.bdh_calib_hbm(kind, p(a), buf2, nbytes, p(rows) if rows is not None else None,  # noqa: E731
-                                         n_rows, stream)
+    def timed(call, reps=10):
         for _ in range(2):
-            if call() != 0:
-                raise RuntimeError(_lib.last_error())
+            call()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 10
         e0.record()
         for _ in range(reps):
             call()
         e1.record()
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
-        out[name] = {"us": round(ms * 1e3, 2), "bytes": moved, "GBs": round(moved / (ms * 1e-3) / 1e9, 1)}
-        print(f"[rmw] {name}: {ms * 1e3:.1f} us, {moved / (ms * 1e-3) / 1e12:.2f} TB/s", flush=True)
+        return e0.elapsed_time(e1) / reps * 1e-3  # seconds
 
-    run("read", _lib.BDH_CALIB_READ, p(sink), None, nbytes)
-    run("copy", _lib.BDH_CALIB_COPY, p(b), None, 2 * nbytes)
-    run("rmw", _lib.BDH_CALIB_RMW, None, None, 2 * nbytes)
+    def calib(kind, buf2, rows, n_rows):
+        st = lib.bdh_calib_hbm(kind, p(a), buf2, nbytes, p(rows) if rows is not None else None, n_rows,
+                               stream)
+        if st != 0:
+            raise RuntimeError(_lib.last_error())
+
+    hbm = {"buffer_bytes": None}
+    nbytes = 64 * 4 * 8192 * 1024
+    hbm["buffer_bytes"] = nbytes
+    a = torch.zeros(nbytes // 4, device="cuda", dtype=torch.float32)
+    b = torch.empty_like(a)
+    sink = torch.zeros(4, device="cuda", dtype=torch.float32)
+
+    def rec(name, sec, moved):
+        hbm[name] = {"us": round(sec * 1e6, 2), "bytes": moved, "GBs": round(moved / sec / 1e9, 1)}
+        print(f"[ceilings] hbm {name}: {sec * 1e6:.1f} us, {moved / sec / 1e12:.2f} TB/s", flush=True)
+
+    rec("read", timed(lambda: calib(_lib.BDH_CALIB_READ, p(sink), None, 0)), nbytes)
+    rec("copy", timed(lambda: calib(_lib.BDH_CALIB_COPY, p(b), None, 0)), 2 * nbytes)
+    rec("rmw", timed(lambda: calib(_lib.BDH_CALIB_RMW, None, None, 0)), 2 * nbytes)
+    rng = np.random.default_rng(SEED + 9)
+    total_rows = nbytes // 1024
     for pct in (5, 10):
         pick = np.sort(rng.choice(total_rows, total_rows * pct // 100, replace=False)).astype(np.int32)
         rows = torch.from_numpy(pick).cuda()
-        run(f"rmw_rows_{pct}pct", _lib.BDH_CALIB_RMW_ROWS, None, rows, 2 * pick.size * 1024)
-    print(json.dumps({"calibration": "hbm", **out}), flush=True)
+        rec(f"rmw_rows_{pct}pct", timed(lambda: calib(_lib.BDH_CALIB_RMW_ROWS, None, rows, pick.size)),
+            2 * pick.size * 1024)
+    rec("torch_copy", timed(lambda: b.copy_(a)), 2 * nbytes)
+    rec("torch_add_inplace", timed(lambda: a.add_(1.0)), 2 * nbytes)
+    del a, b
+
+    mfma = {}
+    flop = ctypes.c_double()
+    for name, kind in (("v_mfma_f32_16x16x32_bf16", _lib.BDH_CALIB_MFMA_16X16X32_BF16),
+                       ("v_mfma_f32_32x32x16_bf16", _lib.BDH_CALIB_MFMA_32X32X16_BF16)):
+        def call():
+            if lib.bdh_calib_mfma(kind, 20000, p(sink), ctypes.byref(flop), stream) != 0:
+                raise RuntimeError(_lib.last_error())
+        sec = timed(call, reps=5)
+        mfma[name] = {"us": round(sec * 1e6, 1), "TFLOPs": round(flop.value / sec / 1e12, 1),
+                      "frac_of_peak": round(flop.value / sec / 1e12 / PEAK_BF16_TFLOPS, 4)}
+        print(f"[ceilings] mfma {name}: {flop.value / sec / 1e12:.0f} TFLOP/s", flush=True)
+
+    blas = {}
+    g = torch.Generator(device="cuda").manual_seed(SEED + 10)
+    q = torch.randn(32, 512, 8192, generator=g, device="cuda").to(torch.bfloat16)
+    qt = q.transpose(1, 2).contiguous()  # a contiguous right operand (no transposed view)
+    v = torch.randn(32, 512, 256, generator=g, device="cuda").to(torch.bfloat16)
+    for name, (x, y) in (("c2_gram", (q, qt)), ("c2_state", (qt, v))):
+        fl = 2.0 * x.shape[0] * x.shape[1] * x.shape[2] * y.shape[2]
+        sec = timed(lambda: torch.bmm(x, y))
+        blas[name] = {"shape": [list(x.shape), list(y.shape)], "us": round(sec * 1e6, 1),
+                      "TFLOPs": round(fl / sec / 1e12, 1)}
+        print(f"[ceilings] hipblaslt {name}: {sec * 1e6:.1f} us, {fl / sec / 1e12:.0f} TFLOP/s", flush=True)
+    del q, qt, v
+    return {"hbm": hbm, "mfma": mfma, "hipblaslt": blas,
+            "peaks": {"hbm_GBs": PEAK_HBM_GBS, "bf16_TFLOPs": PEAK_BF16_TFLOPS}}
 
 
 # --------------------------------------------------------------------------- #
@@ -719,8 +765,8 @@ def main():
     if args.only == "copy":
         bench_copy(torch)
         return
-    if args.only == "rmw":
-        bench_rmw(torch)
+    if args.only in ("rmw", "ceilings"):
+        print(json.dumps({"ceilings": bench_ceilings(torch)}), flush=True)
         return
     pre = bench_prefill(torch, args) if args.only in ("all", "prefill") else None
     dec = bench_decode(torch, args) if args.only in ("all", "decode") else None
@@ -728,6 +774,7 @@ def main():
     mdl = bench_model(torch, args) if args.only in ("all", "model") else None
     mdd = bench_model_decode(torch, args) if args.only in ("all", "model-decode") else None
     f32 = bench_f32(torch, args) if args.only in ("all", "f32") else None
+    ceil = bench_ceilings(torch) if args.only == "all" else None
 
     cpu_pre = cpu_dec = None
     if not args.no_cpu_baseline:
@@ -765,6 +812,8 @@ def main():
             out["model_decode"] = mdd
         if f32 is not None:
             out["fp32_path"] = f32
+        if ceil is not None:
+            out["ceilings"] = ceil
     elif dec is None:
         one = next(r for r in (lng, mdl, mdd, f32) if r is not None)
         out = dict(one, n_gpus=1, higher_is_better=True, scaling="weak", vs_baseline=None,

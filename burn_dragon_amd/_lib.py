@@ -23,6 +23,7 @@ BDH_BF16 = 1
 
 BDH_KERNEL_PREFILL, BDH_KERNEL_DECODE = 0, 1
 BDH_CALIB_READ, BDH_CALIB_COPY, BDH_CALIB_RMW, BDH_CALIB_RMW_ROWS = 0, 1, 2, 3
+BDH_CALIB_MFMA_16X16X32_BF16, BDH_CALIB_MFMA_32X32X16_BF16 = 0, 1
 BDH_ROPE_SEQUENTIAL = 0
 BDH_ROPE_FIXED = 1
 
@@ -96,6 +97,7 @@ SIGNATURES = {
     "bdh_scratch_release": (_i32, [_vp]),
     "bdh_selftest_rot8": (_i32, [_vp] * 6 + [_i64, _vp]),
     "bdh_calib_hbm": (_i32, [_i32, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "bdh_calib_mfma": (_i32, [_i32, _i64, _vp, _vp, _vp]),
     "bdh_last_error": (ctypes.c_char_p, []),
     "bdh_version": (ctypes.c_char_p, []),
 }

@@ -364,8 +364,10 @@ bdh_status bdh_selftest_rot8(const void* x, const void* cs, void* out_bf16_asm,
  *   BDH_CALIB_COPY      buf -> buf2
  *   BDH_CALIB_RMW       buf[i] += (1, 0, 0, 0) in place
  *   BDH_CALIB_RMW_ROWS  the same on the 1 KiB rows rows[0..n_rows) of buf,
- *                       one wavefront per row; indices outside
- *                       [0, bytes / 1024) are skipped. */
+ *                       one wavefront per row (four in flight), written
+ *                       back with non-temporal stores as the decode step
+ *                       does; indices outside [0, bytes / 1024) are
+ *                       skipped. */
 typedef enum {
   BDH_CALIB_READ = 0,
   BDH_CALIB_COPY = 1,
@@ -374,6 +376,18 @@ typedef enum {
 } bdh_calib_kind;
 bdh_status bdh_calib_hbm(int32_t kind, void* buf, void* buf2, int64_t bytes, const int32_t* rows,
                          int64_t n_rows, void* stream);
+
+/* MFMA calibration hook, no counterpart in the reference: one launch of
+ * `iters` rounds of one bf16 MFMA shape on register operands (8 independent
+ * accumulator chains per wave, two waves per SIMD on every CU), the matrix
+ * core rate the prefill kernels are read against.  *flop_out receives the
+ * launch's FLOP (2 m n k per MFMA); sink is a 4-byte buffer that is never
+ * written for these operands. */
+typedef enum {
+  BDH_CALIB_MFMA_16X16X32_BF16 = 0,
+  BDH_CALIB_MFMA_32X32X16_BF16 = 1
+} bdh_calib_mfma_kind;
+bdh_status bdh_calib_mfma(int32_t kind, int64_t iters, float* sink, double* flop_out, void* stream);
 
 /* Thread-local message of the last non-OK status of this thread. */
 const char* bdh_last_error(void);

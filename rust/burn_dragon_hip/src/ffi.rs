@@ -21,6 +21,8 @@ pub const BDH_CALIB_READ: i32 = 0;
 pub const BDH_CALIB_COPY: i32 = 1;
 pub const BDH_CALIB_RMW: i32 = 2;
 pub const BDH_CALIB_RMW_ROWS: i32 = 3;
+pub const BDH_CALIB_MFMA_16X16X32_BF16: i32 = 0;
+pub const BDH_CALIB_MFMA_32X32X16_BF16: i32 = 1;
 
 #[repr(C)]
 #[derive(Clone, Copy, Debug, Default)]
@@ -153,6 +155,8 @@ extern "C" {
                              out_f32_builtin: *mut f32, n_chunks: i64, stream: *mut c_void) -> i32;
     pub fn bdh_calib_hbm(kind: i32, buf: *mut c_void, buf2: *mut c_void, bytes: i64,
                          rows: *const i32, n_rows: i64, stream: *mut c_void) -> i32;
+    pub fn bdh_calib_mfma(kind: i32, iters: i64, sink: *mut f32, flop_out: *mut f64,
+                          stream: *mut c_void) -> i32;
     pub fn bdh_last_error() -> *const c_char;
     pub fn bdh_version() -> *const c_char;
 }

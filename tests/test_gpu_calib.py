@@ -46,3 +46,26 @@ def test_calibration_kernels_do_the_credited_work():
     assert torch.equal(a.view(rows_total, 64, 4), want)
     assert lib.bdh_calib_hbm(_lib.BDH_CALIB_RMW, p(a), None, 1000, None, 0, stream) == _lib.BDH_EINVAL
     assert lib.bdh_calib_hbm(7, p(a), None, nbytes, None, 0, stream) == _lib.BDH_EINVAL
+
+
+def test_mfma_calibration_reports_its_flop():
+    torch = need_gpu()
+    from burn_dragon_amd import _lib
+    lib = _lib.load()
+    sink = torch.zeros(4, device="cuda")
+    flop = ctypes.c_double()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    announce("calib mfma")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for kind, per_mfma, per_round in ((_lib.BDH_CALIB_MFMA_16X16X32_BF16, 2 * 16 * 16 * 32, 8),
+                                      (_lib.BDH_CALIB_MFMA_32X32X16_BF16, 2 * 32 * 32 * 16, 4)):
+        assert lib.bdh_calib_mfma(kind, 100, ctypes.c_void_p(sink.data_ptr()), ctypes.byref(flop),
+                                  stream) == _lib.BDH_OK
+        torch.cuda.synchronize()
+        # two 4-wave workgroups per CU, `per_round` MFMAs a round, 100 rounds
+        assert flop.value == 2 * cus * 4 * 100 * per_round * per_mfma
+        assert torch.equal(sink, torch.zeros_like(sink))
+    assert lib.bdh_calib_mfma(5, 100, ctypes.c_void_p(sink.data_ptr()), ctypes.byref(flop),
+                              stream) == _lib.BDH_EINVAL
+    assert lib.bdh_calib_mfma(0, 0, ctypes.c_void_p(sink.data_ptr()), ctypes.byref(flop),
+                              stream) == _lib.BDH_EINVAL

@@ -147,3 +147,41 @@ def test_decode_step_with_pointers_off_16_byte_alignment(oracle):
     partner = x.reshape(B, H, N // 2, 2)[..., ::-1].reshape(B, H, N)
     untouched = (x == 0) & (partner == 0)
     assert np.array_equal(host(rd)[untouched], rho0[untouched])
+
+
+@pytest.mark.parametrize("B,H,N,D,pos,density", [
+    (64, 4, 256, 16, 9, 0.02),      # 256 streams of a few rows each
+    (1, 1, 65536, 64, 3, 0.3),      # one long stream (several compaction passes)
+    (8, 16, 512, 32, 77, 0.0),      # no active row at all
+    (2048, 1, 64, 8, 5, 0.05),      # many short streams
+    (2049, 1, 32, 8, 6, 0.1),
+])
+def test_decode_stream_counts(oracle, B, H, N, D, pos, density):
+    # Streams with few, many or no active rows, one stream alone and over two
+    # thousand streams: every readout, row and list matches the oracle, and
+    # the step without lists equals the step with them.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(5000 + N + B)
+    x = (rng.random((B, H, N)) < density).astype(np.float32) * rng.random((B, H, N)).astype(np.float32)
+    x[::3] = 0.0  # whole streams without an active row between active ones
+    v = rc.gaussian(rng, (B, 1, D), 1 / 16)
+    rho0 = rc.gaussian(rng, (B, H, N, D), 0.5)
+    rho_ref = rho0.copy()
+    a_ref, idx_ref, cnt_ref = oracle.decode_step_f32(x, v, rho_ref, pos)
+    announce("decode stream counts", B, H, N, D, pos, density)
+    rho_d = dev(torch, rho0)
+    out = bd.decode_step(dev(torch, x), dev(torch, v), rho_d, position=pos, want_active=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.active_cnt.cpu().numpy(), cnt_ref)
+    assert np.array_equal(out.active_idx.cpu().numpy(), idx_ref)
+    a = host(out.readout)
+    assert np.all(a[cnt_ref == 0] == 0.0)
+    if np.abs(a_ref).sum() > 0:
+        assert rel_l2(a, a_ref) <= TOL_F32
+    assert rel_l2(host(rho_d), rho_ref) <= TOL_F32
+    # and without the lists (the step keeps its own)
+    rho_d2 = dev(torch, rho0)
+    out2 = bd.decode_step(dev(torch, x), dev(torch, v), rho_d2, position=pos)
+    torch.cuda.synchronize()
+    assert torch.equal(out2.readout, out.readout) and torch.equal(rho_d2, rho_d)
