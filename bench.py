@@ -73,13 +73,14 @@ def parse():
 
 
 # --------------------------------------------------------------------------- #
-def lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho, chunk=0):
+def lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho, chunk=0, decay=None):
     """One RoPE-fused bf16 forward; chunk = the row chunk (rho materialised
-    every `chunk` tokens, 0 = 512)."""
+    every `chunk` tokens, 0 = 512); decay [H] f32 on the device or None."""
     from burn_dragon_amd import _lib
     st = lib.bdh_recurrent_attention_rope_fwd(
         ctypes.byref(plan), _lib.BDH_BF16, ctypes.c_void_p(x.data_ptr()),
-        ctypes.c_void_p(v.data_ptr()), None, None, ctypes.byref(rope),
+        ctypes.c_void_p(v.data_ptr()), None,
+        ctypes.c_void_p(decay.data_ptr()) if decay is not None else None, ctypes.byref(rope),
         ctypes.c_void_p(ctx.data_ptr()), ctypes.c_void_p(rho.data_ptr()), chunk,
         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     if st != 0:
@@ -238,6 +239,17 @@ def bench_long(torch, args):
     e1.record()
     torch.cuda.synchronize()
     ms_c = e0.elapsed_time(e1) / steps
+    # The same call with ALiBi-style decay per head (the state-carry form with
+    # decay: weighted q^T rows, the carried block scaled per interval).
+    dk = torch.tensor([0.999, 0.998, 0.997, 0.996], device=dev, dtype=torch.float32)
+    for _ in range(2):
+        lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho, decay=dk)
+    e0.record()
+    for _ in range(steps):
+        lib_fwd_call(torch, lib, plan, x, v, rope, ctx, rho, decay=dk)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_d = e0.elapsed_time(e1) / steps
     flop = B * H * T * (4 * N * D + (C - 1) * (N + D))
     call_tflops = flop / (ms * 1e-3) / 1e12
     # The dominant kernels: a call's state-carry launch and its gram/readout
@@ -249,7 +261,8 @@ def bench_long(torch, args):
     achieved = k_flop / (k_ms * 1e-3) / 1e12
     print(f"[long] {ms:.3f} ms/prefill, {B * T / (ms * 1e-3) / 1e6:.2f} M tok/s, "
           f"{call_tflops:.1f} TFLOP/s per call; carry + snap_wide kernels {k_n:.0f} launches, "
-          f"{k_ms:.3f} ms, {achieved:.1f} TFLOP/s; at row chunk {C}: {ms_c:.3f} ms", flush=True)
+          f"{k_ms:.3f} ms, {achieved:.1f} TFLOP/s; at row chunk {C}: {ms_c:.3f} ms; with decay: "
+          f"{ms_d:.3f} ms", flush=True)
     return {"metric": "C4 long-context prefill tokens/s per BDH layer", "value": B * T / (ms * 1e-3),
             "unit": "tokens/s", "ms_per_prefill": ms, "steps": steps,
             "config": {"workload": "C4 long prefill, one BDH layer: B1 nh4 T8192 N8192 D256, "
@@ -258,6 +271,8 @@ def bench_long(torch, args):
                                    f"chunk {C}"},
             "at_config_chunk": {"chunk": C, "ms_per_prefill": round(ms_c, 4),
                                 "tokens_per_s": round(B * T / (ms_c * 1e-3), 1)},
+            "with_decay": {"decay": [0.999, 0.998, 0.997, 0.996], "ms_per_prefill": round(ms_d, 4),
+                           "tokens_per_s": round(B * T / (ms_d * 1e-3), 1)},
             "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                          "traffic": TRAFFIC_LONG_C4,

@@ -302,14 +302,13 @@ bdh_status check_plan(const bdh_recurrent_plan* p) {
 // default 512 at config.rs:10, used as linear.rs:117-118 uses it), shortened
 // to the call's length rounded up to 128.
 constexpr int64_t kMaxRowChunk = 4096;
-// Row chunk 0 = auto: 512, the reference's default.  With decay (the
-// per-interval launch chain) 1024 from 4096 tokens on: halving the launches
-// pays for the longer score blocks (T = 8192, N = 8192, D = 256: 1.13 ms per
-// call against 1.22 ms at 512).  Without decay (the state-carry form) 512
-// stays faster: the gram work grows with the chunk, the snapshots shrink
-// with it (C4: 0.74 ms at 512, 0.77 at 768, 0.81 at 1024).
+// Row chunk 0 = auto: 512, the reference's default, which is also the
+// fastest of the state-carry form (with or without decay): the gram work
+// grows with the chunk, the snapshots shrink with it (C4: 0.74 ms at 512,
+// 0.77 at 768, 0.81 at 1024).
 int64_t state_interval(int64_t T, int32_t chunk, bool decay) {
-  const int64_t L = chunk > 0 ? chunk : (decay && T >= 4096 ? 1024 : 512);
+  (void)decay;
+  const int64_t L = chunk > 0 ? chunk : 512;
   return T < L ? ((T + 127) / 128) * 128 : L;
 }
 

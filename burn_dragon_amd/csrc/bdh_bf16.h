@@ -198,6 +198,7 @@ struct CarryArgs {
   float* rho_out;       // [S, N, D] (may be rho_in)
   bf16_t* snap;         // [n_iv, S, D, N]
   bf16_t* q;            // [S, T, N] rotated queries (freqs set)
+  const float* decay;   // [H] or null (ones)
 };
 int prefill_carry_units(int64_t S, int64_t N, int64_t Dp);
 // Gram and readout tiles of the state-carry form in 8-wave workgroups

@@ -1,16 +1,20 @@
 // State-carry kernel of the multi-interval bf16 prefill (gfx950 MFMA).
 //
 // With two or more state-carry intervals the state at each interval start,
-// rho_iv = rho_in + sum_{iv' < iv} Q_iv'^T V_iv', is what the readouts of
-// interval iv need.  Without decay the update of a (stream, 128-neuron,
-// 256-column) block of rho depends only on that block, so one workgroup owns
-// the block and walks every token of the call with it in its accumulators:
+// rho_iv = rho_in d^(t_iv) + sum_{iv' < iv} (Q_iv' * d^(end - t))^T V_iv'
+// (d = 1 without decay), is what the readouts of interval iv need.  The
+// update of a (stream, 128-neuron, 256-column) block of rho depends only on
+// that block, so one workgroup owns the block and walks every token of the
+// call with it in its accumulators:
 //   - per 32-token step it loads x (and rotates it: q = RoPE(x), each x
 //     element read and rotated once per call), writes q for the gram and
 //     readout units of the next launch (first column block only), stages
 //     q^T and v^T in LDS and accumulates q^T v with v_mfma_f32_16x16x32_bf16;
 //   - at each interval boundary it writes its block of rho_iv as bf16,
-//     transposed ([d][n]: the operand layout of the readout units);
+//     transposed ([d][n]: the operand layout of the readout units), and with
+//     decay scales the block by d^Lc, Lc the new interval's length, while
+//     each token's q^T row is weighted by d^(end - t), end the token's
+//     interval end (recurrent.rs:415 over an interval; linear.rs:105-197);
 //   - at the end it writes the final rho in f32.
 // The readouts of every interval and the gram tiles then run in one launch
 // (snap_wide_kernel), with no chain of per-interval launches and no f32
@@ -60,7 +64,7 @@ __device__ __forceinline__ void lds_dma_wait_barrier() {
 __device__ __forceinline__ void plain_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // The loading waves (rw = wave - 4).
-template <bool ROPE, bool QOUT>
+template <bool ROPE, bool QOUT, bool DECAY>
 __device__ __forceinline__ void carry_loader(const CarryArgs& a, char* lds, int64_t s, int64_t n0, int64_t d0,
                                              int rw, int lane) {
   const int rtid = rw * 64 + lane;
@@ -109,34 +113,71 @@ __device__ __forceinline__ void carry_loader(const CarryArgs& a, char* lds, int6
   float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (ROPE) load_freq4(a.freqs + n0 + 8 * nv, fq);
   // q^T of step k (tokens 2 tp, 2 tp + 1 of neuron 8 nv + e) into buffer k & 1.
+  const float dk = DECAY ? a.decay[h] : 1.0f;
+  const float l2d = DECAY ? decay_log2(dk) : 0.0f;
+  // Weight of token t's row of q^T: d^(end - t), end the end of t's
+  // interval; tokens past T (zero v^T columns) weigh 0, so no power of d
+  // beyond its interval is formed.
+  auto weight = [&](int64_t t) -> float {
+    if (t >= a.T) return 0.0f;
+    const int64_t e = (t / a.L + 1) * a.L;
+    return decay_pow_int(dk, l2d, (int)((e < a.T ? e : a.T) - t));
+  };
   auto rotate = [&](int kt, int slot) {
     char* R = lds + slot * CARRY_STAGE;
     const int r0 = 2 * tp, r1 = 2 * tp + 1;
     uint4* X0 = reinterpret_cast<uint4*>(R + r0 * 256 + ((nv ^ (r0 & 15)) << 4));
     uint4* X1 = reinterpret_cast<uint4*>(R + r1 * 256 + ((nv ^ (r1 & 15)) << 4));
-    uint4 q0 = *X0, q1 = *X1;
+    const uint4 x0 = *X0, x1 = *X1;
+    uint4 q0 = x0, q1 = x1;    // rotated: the rows the gram and readout tiles read
+    uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
+    const int64_t t = (int64_t)kt * BK + 2 * tp;
     if (ROPE) {
       // Tokens past T hold row T - 1 (see issue) and are rotated at its
       // position, so their q is row T - 1's; their v^T columns are zero, so
       // they add nothing to rho.  Sums of integers below 2^24 are exact in f32.
-      const int64_t t = (int64_t)kt * BK + 2 * tp;
       const int64_t ta = t < a.T ? t : a.T - 1, tb = t + 1 < a.T ? t + 1 : a.T - 1;
       const float pa = (float)(a.fixed ? a.pos0 : a.pos0 + ta);
       const float pb = (float)(a.fixed ? a.pos0 : a.pos0 + tb);
-      q0 = rot8_bf16(q0, rope_cs4(pa, fq));
-      q1 = rot8_bf16(q1, rope_cs4(pb, fq));
+      c0 = rope_cs4(pa, fq);
+      c1 = rope_cs4(pb, fq);
+    }
+    uint4 u0, u1;  // the q^T source rows: rotated and, with decay, weighted
+    if (DECAY) {
+      // Weighted from the f32 rotation, rounded once.
+      float f0[8], f1[8];
+      prep8_f32<ROPE>(x0, c0, 1.0f, false, f0);
+      prep8_f32<ROPE>(x1, c1, 1.0f, false, f1);
+      if (ROPE) {
+        q0 = make_uint4(pack_bf16x2(f0[0], f0[1]), pack_bf16x2(f0[2], f0[3]), pack_bf16x2(f0[4], f0[5]),
+                        pack_bf16x2(f0[6], f0[7]));
+        q1 = make_uint4(pack_bf16x2(f1[0], f1[1]), pack_bf16x2(f1[2], f1[3]), pack_bf16x2(f1[4], f1[5]),
+                        pack_bf16x2(f1[6], f1[7]));
+      }
+      const float w0 = weight(t), w1 = weight(t + 1);
+      u0 = make_uint4(pack_bf16x2(f0[0] * w0, f0[1] * w0), pack_bf16x2(f0[2] * w0, f0[3] * w0),
+                      pack_bf16x2(f0[4] * w0, f0[5] * w0), pack_bf16x2(f0[6] * w0, f0[7] * w0));
+      u1 = make_uint4(pack_bf16x2(f1[0] * w1, f1[1] * w1), pack_bf16x2(f1[2] * w1, f1[3] * w1),
+                      pack_bf16x2(f1[4] * w1, f1[5] * w1), pack_bf16x2(f1[6] * w1, f1[7] * w1));
+    } else {
+      if (ROPE) {
+        q0 = rot8_bf16(x0, c0);
+        q1 = rot8_bf16(x1, c1);
+      }
+      u0 = q0;
+      u1 = q1;
     }
     if (QOUT) {  // back in place for the q stores (each thread rewrites only what it read)
       *X0 = q0;
       *X1 = q1;
     }
     // q^T: word (neuron e, tokens 2 tp, 2 tp + 1) from the two tokens' words.
-    const uint32_t u0[4] = {q0.x, q0.y, q0.z, q0.w}, u1[4] = {q1.x, q1.y, q1.z, q1.w};
+    const uint32_t w0[4] = {u0.x, u0.y, u0.z, u0.w}, w1[4] = {u1.x, u1.y, u1.z, u1.w};
     uint32_t* Aw = reinterpret_cast<uint32_t*>(lds + CARRY_XT + (kt & 1) * 8192);
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      Aw[(lds_off(8 * nv + 2 * p, tp >> 2) + 2 * (tp & 3)) >> 1] = (u0[p] & 0xffffu) | (u1[p] << 16);
-      Aw[(lds_off(8 * nv + 2 * p + 1, tp >> 2) + 2 * (tp & 3)) >> 1] = (u0[p] >> 16) | (u1[p] & 0xffff0000u);
+      Aw[(lds_off(8 * nv + 2 * p, tp >> 2) + 2 * (tp & 3)) >> 1] = (w0[p] & 0xffffu) | (w1[p] << 16);
+      Aw[(lds_off(8 * nv + 2 * p + 1, tp >> 2) + 2 * (tp & 3)) >> 1] = (w0[p] >> 16) | (w1[p] & 0xffff0000u);
     }
   };
   // Every load above has completed before the ring starts (the compiler cannot
@@ -159,7 +200,7 @@ __device__ __forceinline__ void carry_loader(const CarryArgs& a, char* lds, int6
 }
 
 // The multiplying waves (w = 0..3): rows n0 + 64 wm .., columns d0 + 128 wn ..
-template <bool QOUT>
+template <bool QOUT, bool DECAY>
 __device__ __forceinline__ void carry_mma(const CarryArgs& a, char* lds, int64_t s, int64_t n0, int64_t d0, int w,
                                           int lane) {
   const int wm = w >> 1, wn = w & 1;
@@ -201,7 +242,25 @@ __device__ __forceinline__ void carry_mma(const CarryArgs& a, char* lds, int64_t
                          pack_bf16x2(acc[mi][ni][2], acc[mi][ni][3]));
       }
   };
-  if (a.rho_in) snapshot(0);
+  // With decay: the carried block times d^Lc at the start of interval iv
+  // (Lc its length), the weighted q^T rows of the interval being added after.
+  const float dk = DECAY ? a.decay[s % a.H] : 1.0f;
+  const float l2d = DECAY ? decay_log2(dk) : 0.0f;
+  auto carry_scale = [&](int64_t iv) {
+    if (!DECAY) return;
+    const int64_t t0 = iv * a.L;
+    const float f = decay_pow_int(dk, l2d, (int)(a.T - t0 < a.L ? a.T - t0 : a.L));
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mi][ni][r] *= f;
+  };
+  if (a.rho_in) {
+    snapshot(0);
+    carry_scale(0);
+  }
   bf16_t* Q = QOUT ? a.q + s * a.T * a.N : nullptr;
   // q rows of step k from its ring slot (rotated in place) to HBM: lane
   // (lane & 15) stores chunk c of rows 4 (w + 4 j) + (lane >> 4), so each
@@ -232,7 +291,10 @@ __device__ __forceinline__ void carry_mma(const CarryArgs& a, char* lds, int64_t
                        reinterpret_cast<const bf16_t*>(lds + (k % CARRY_R) * CARRY_STAGE + 8192), lane, 64 * wm,
                        128 * wn, acc);
     if (QOUT) store_q(k, k % CARRY_R);
-    if ((k + 1) % spi == 0 && k + 1 < nk) snapshot((k + 1) / spi);
+    if ((k + 1) % spi == 0 && k + 1 < nk) {
+      snapshot((k + 1) / spi);
+      carry_scale((k + 1) / spi);
+    }
   }
   lds_dma_wait_barrier<0>();  // the epilogue reuses the ring
 
@@ -244,14 +306,14 @@ __device__ __forceinline__ void carry_mma(const CarryArgs& a, char* lds, int64_t
   });
 }
 
-template <bool ROPE, bool QOUT>
+template <bool ROPE, bool QOUT, bool DECAY>
 __device__ __forceinline__ void carry_unit(const CarryArgs& a, char* lds, int64_t s, int64_t n0, int64_t d0) {
   const int lane = threadIdx.x & 63, w = wave_id();
-  if (w >= 4) carry_loader<ROPE, QOUT>(a, lds, s, n0, d0, w - 4, lane);
-  else carry_mma<QOUT>(a, lds, s, n0, d0, w, lane);
+  if (w >= 4) carry_loader<ROPE, QOUT, DECAY>(a, lds, s, n0, d0, w - 4, lane);
+  else carry_mma<QOUT, DECAY>(a, lds, s, n0, d0, w, lane);
 }
 
-template <bool ROPE>
+template <bool ROPE, bool DECAY>
 __global__ __launch_bounds__(CARRY_NT, 1) void prefill_carry_kernel(CarryArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[CARRY_LDS];
   const int nt = (int)(a.N / CARRY_N);
@@ -265,8 +327,8 @@ __global__ __launch_bounds__(CARRY_NT, 1) void prefill_carry_kernel(CarryArgs a)
   const int64_t s = u / (nt * dt);
   const int rem = u - (int)s * nt * dt;
   const int64_t n0 = (int64_t)(rem / dt) * CARRY_N, d0 = (int64_t)(rem % dt) * T256;
-  if (ROPE && d0 == 0) carry_unit<ROPE, true>(a, lds, s, n0, d0);
-  else carry_unit<ROPE, false>(a, lds, s, n0, d0);
+  if (ROPE && d0 == 0) carry_unit<ROPE, true, DECAY>(a, lds, s, n0, d0);
+  else carry_unit<ROPE, false, DECAY>(a, lds, s, n0, d0);
 }
 
 }  // namespace
@@ -275,8 +337,13 @@ int prefill_carry_units(int64_t S, int64_t N, int64_t Dp) { return (int)(S * (N 
 
 hipError_t launch_prefill_carry(const CarryArgs& a, hipStream_t st) {
   const unsigned grid = (unsigned)prefill_carry_units(a.S, a.N, a.Dp);
-  if (a.freqs) hipLaunchKernelGGL((prefill_carry_kernel<true>), dim3(grid), dim3(CARRY_NT), 0, st, a);
-  else hipLaunchKernelGGL((prefill_carry_kernel<false>), dim3(grid), dim3(CARRY_NT), 0, st, a);
+  if (a.decay) {
+    if (a.freqs) hipLaunchKernelGGL((prefill_carry_kernel<true, true>), dim3(grid), dim3(CARRY_NT), 0, st, a);
+    else hipLaunchKernelGGL((prefill_carry_kernel<false, true>), dim3(grid), dim3(CARRY_NT), 0, st, a);
+  } else {
+    if (a.freqs) hipLaunchKernelGGL((prefill_carry_kernel<true, false>), dim3(grid), dim3(CARRY_NT), 0, st, a);
+    else hipLaunchKernelGGL((prefill_carry_kernel<false, false>), dim3(grid), dim3(CARRY_NT), 0, st, a);
+  }
   return hipGetLastError();
 }
 

@@ -445,6 +445,7 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   c.rho_out = a.rho_out;
   c.snap = (bf16_t*)snap;
   c.q = (bf16_t*)q;
+  c.decay = a.decay;
   int kt = ktime_begin(BDH_KERNEL_PREFILL, st);
   BDH_HIP_TRY(launch_prefill_carry(c, st));
   ktime_end(kt, st);
@@ -454,7 +455,7 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   p.freqs = nullptr;
   p.pos0 = a.pos0;
   p.fixed = a.fixed;
-  p.decay = nullptr;
+  p.decay = a.decay;
   p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;
   p.part = (float*)part;
   p.L = L; p.Lp = Lp; p.n_iv = n_iv;
@@ -551,7 +552,7 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
   const int nk = (int)(a.N / 32);  // 32-deep gram steps
   const int state_units = prefill_state_units(S, a.N, a.D);
   // (The readout units address a snapshot's rows with 32-bit offsets.)
-  if (a.state && n_iv >= 2 && a.decay == nullptr && a.D * a.N * 2 < ((int64_t)1 << 31) &&
+  if (a.state && n_iv >= 2 && a.D * a.N * 2 < ((int64_t)1 << 31) &&
       (size_t)(n_iv * S * a.N * a.D) * sizeof(bf16_t) <= kCarrySnapMax)
     return run_carry_path(a, st, launches, S, Tp, Dp, n_iv, Lp, nb, nk);
   if (!a.state && a.rho_in == nullptr && a.freqs == nullptr && a.decay == nullptr && n_iv == 1)

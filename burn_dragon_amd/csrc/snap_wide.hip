@@ -1,5 +1,8 @@
-// Gram and readout tiles of the state-carry form (two or more intervals, no
-// decay, q already rotated) in 512-thread workgroups (8 waves, one per CU).
+// Gram and readout tiles of the state-carry form (two or more intervals, q
+// already rotated) in 512-thread workgroups (8 waves, one per CU).  With
+// decay d the epilogues apply the closed form's powers: d^(r - c) to the
+// score (r, c) below the diagonal, d^r to readout row r (r, c local to the
+// interval: linear.rs:105-197).
 //
 // Every operand row comes from HBM (or L2) through a four-stage direct-load
 // LDS ring, so what bounds these tiles is the operand traffic per MFMA.  A
@@ -173,12 +176,21 @@ __device__ __forceinline__ void snap_wide_unit(const PrefillArgs& a, bf16_t* lds
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the last (unused) fragment reads
   dma_wait_barrier<0>();  // the epilogue reuses the ring
 
+  const float dk = a.decay ? a.decay[s % a.H] : 1.0f;
+  const float l2d = a.decay ? decay_log2(dk) : 0.0f;
   if (KIND == K_READ) {
     float* P = a.rd_part + ((int64_t)kp * a.S + s) * a.T * a.D + t0 * a.D;
     epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
       const int64_t t = wr0 + row, d = wc0 + col;
-      if (active && t < Lc && d < a.D)
-        __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, reinterpret_cast<floatx4*>(&P[t * a.D + d]));
+      if (!active || t >= Lc || d >= a.D) return;
+      if (a.decay) {
+        const float f = decay_pow_int(dk, l2d, (int)t);
+        v.x *= f;
+        v.y *= f;
+        v.z *= f;
+        v.w *= f;
+      }
+      __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, reinterpret_cast<floatx4*>(&P[t * a.D + d]));
     });
   } else {
     // Scores of rows ti < Lc and columns tj < Lc, 0 on and above the
@@ -187,8 +199,13 @@ __device__ __forceinline__ void snap_wide_unit(const PrefillArgs& a, bf16_t* lds
     epilogue_64x128(acc, lds, w, lane, [&](int row, int col, float4 v) {
       const int64_t ti = wr0 + row, tj = wc0 + col;
       if (!active || ti >= Lc) return;
-      const float e[4] = {tj < ti ? v.x : 0.0f, tj + 1 < ti ? v.y : 0.0f, tj + 2 < ti ? v.z : 0.0f,
-                          tj + 3 < ti ? v.w : 0.0f};
+      float e[4] = {tj < ti ? v.x : 0.0f, tj + 1 < ti ? v.y : 0.0f, tj + 2 < ti ? v.z : 0.0f,
+                    tj + 3 < ti ? v.w : 0.0f};
+      if (a.decay) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (tj + j < ti) e[j] *= decay_pow_int(dk, l2d, (int)(ti - tj - j));
+      }
       float* dst = P + ti * a.Lp + tj;
       if (tj + 3 < Lc) {
         __builtin_nontemporal_store(floatx4{e[0], e[1], e[2], e[3]}, reinterpret_cast<floatx4*>(dst));

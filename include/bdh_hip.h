@@ -97,7 +97,7 @@ int32_t bdh_supports_backend(void);
  * dense_score_row_chunk (config.rs:46; linear.rs:117-118): rho is
  * materialised every `chunk` tokens and the carries inside a row chunk go
  * through causal score blocks of 128 tokens.  0 = auto: 512 (the
- * reference's default, config.rs:10), with decay 1024 from time >= 4096; otherwise a
+ * reference's default, config.rs:10), with or without decay; otherwise a
  * multiple of 128 up to 4096 (BDH_UNSUPPORTED otherwise).  The result does
  * not depend on it beyond rounding; the fp32 path materialises rho every 256
  * tokens whatever it is.

@@ -5,8 +5,9 @@ every stream:
     one call (state carry across chunks and intervals);
   * C3 (B64 decode): rows outside the active set are bit-identical after a
     step, sampled streams match the oracle, active sets bit-exact;
-  * C4 (B1 T8192 chunk 256 bf16): every chunk boundary and the final rho
-    against the oracle for all four heads."""
+  * C4 (B1 T8192 bf16) at the automatic row chunk and at the config's chunk
+    256: every chunk boundary and the final rho against the oracle for all
+    four heads; with decay, two heads."""
 import numpy as np
 import pytest
 
@@ -95,22 +96,52 @@ def test_c3_decode_full_size(oracle):
 
 
 def test_c4_long_context_full_size(oracle):
+    # The automatic row chunk (512) and the config's chunk 256 (31 bf16 rho
+    # snapshots), both against one oracle run: every chunk boundary, the whole
+    # context and the final rho of all four heads.
     torch = need_gpu()
     import burn_dragon_amd as bd
     B, H, T, N, D = 1, 4, 8192, 8192, 256
     x, v = _bf16_inputs(torch, rc.config_seed(4), B, H, T, N, D)
-    announce("C4 long prefill")
-    out = bd.try_fused_recurrent_attention_rope(x, v, position=0)
-    torch.cuda.synchronize()
     q = oracle.rope_rotate(host(x), pos0=0)
     cref, rref = oracle.recurrent_f64(q, host(v))
-    ctx = host(out.context)
     bounds = sorted({t for c in range(1, T // 256) for t in (256 * c - 1, 256 * c)} | {T - 1})
-    e_b = rel_l2(ctx[:, :, bounds], cref[:, :, bounds])
-    e_all = rel_l2(ctx, cref)
-    e_rho = rel_l2(host(out.rho), rref)
-    print(f"C4 rel-L2 boundaries {e_b:.2e} all {e_all:.2e} rho {e_rho:.2e}")
-    assert e_b <= TOL_BF16 and e_all <= TOL_BF16 and e_rho <= TOL_BF16
+    for chunk in (0, 256):
+        announce("C4 long prefill", chunk)
+        out = bd.try_fused_recurrent_attention_rope(x, v, position=0, chunk=chunk)
+        torch.cuda.synchronize()
+        ctx = host(out.context)
+        e_b = rel_l2(ctx[:, :, bounds], cref[:, :, bounds])
+        e_all = rel_l2(ctx, cref)
+        e_rho = rel_l2(host(out.rho), rref)
+        print(f"C4 chunk {chunk} rel-L2 boundaries {e_b:.2e} all {e_all:.2e} rho {e_rho:.2e}")
+        assert e_b <= TOL_BF16 and e_all <= TOL_BF16 and e_rho <= TOL_BF16
+        del out
+
+
+def test_c4_long_context_with_decay_full_size(oracle):
+    # C4's shape with ALiBi-like decay per head (the state-carry form with
+    # decay): heads 0 and 3 against the oracle, at every chunk boundary and
+    # on the final rho.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    B, H, T, N, D = 1, 4, 8192, 8192, 256
+    x, v = _bf16_inputs(torch, rc.config_seed(4) + 7, B, H, T, N, D)
+    dec = np.array([0.999, 0.998, 0.997, 0.996], np.float32)
+    announce("C4 long prefill with decay")
+    out = bd.try_fused_recurrent_attention_rope(x, v, decay=torch.from_numpy(dec).cuda(), position=0)
+    torch.cuda.synchronize()
+    assert out is not None
+    xh, vh = host(x), host(v)
+    bounds = sorted({t for c in range(1, T // 256) for t in (256 * c - 1, 256 * c)} | {T - 1})
+    for h in (0, 3):
+        q = oracle.rope_rotate(xh[:, h:h + 1], pos0=0)
+        cref, rref = oracle.recurrent_f64(q, vh, None, dec[h:h + 1])
+        ctx = host(out.context[:, h:h + 1])
+        e_b = rel_l2(ctx[:, :, bounds], cref[:, :, bounds])
+        e_rho = rel_l2(host(out.rho[:, h:h + 1]), rref)
+        print(f"C4 decay head {h} rel-L2 boundaries {e_b:.2e} all {rel_l2(ctx, cref):.2e} rho {e_rho:.2e}")
+        assert e_b <= TOL_BF16 and rel_l2(ctx, cref) <= TOL_BF16 and e_rho <= TOL_BF16
 
 
 def test_c3_decode_after_1024_token_prefill(oracle):

@@ -210,6 +210,40 @@ def test_bf16_row_chunk(oracle, chunk):
     assert rel_l2(host(out.context), cref) <= TOL_BF16 and rel_l2(host(out.rho), rref) <= TOL_BF16
 
 
+@pytest.mark.parametrize("rope,decay,chunk,T", [
+    (None, [0.9, -0.8], 256, 700),        # pre-rotated queries, a negative decay, 3 intervals
+    ((6, False), [0.5, 0.25], 128, 1100),  # strong decay: powers underflow inside an interval
+    ((0, False), [1.0, 0.97], 384, 900),   # a decay of exactly 1 beside a decaying head
+])
+def test_bf16_state_carry_with_decay(oracle, rope, decay, chunk, T):
+    # Decay in the state-carry form (two or more intervals): each token's row
+    # of q^T weighted by d^(end - t), the carried block scaled by d^Lc at
+    # each interval start, d^(r - c) on the scores and d^r on the readouts.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(83 + T + chunk)
+    x, v, rho0 = _bf16_case(rng, 1, 2, 1, T, 256, 64, True)
+    dec = np.array(decay, np.float32)
+    xb, vb = oracle.round_bf16(x), oracle.round_bf16(v)
+    if rope is None:
+        xb = oracle.round_bf16(oracle.rope_rotate(xb, pos0=0))
+    announce("bf16 state carry decay", rope, decay, chunk, T)
+    xd, vd = dev(torch, xb, torch.bfloat16), dev(torch, vb, torch.bfloat16)
+    if rope is None:
+        out = bd.try_fused_recurrent_attention(xd, vd, dev(torch, rho0), dev(torch, dec), chunk=chunk)
+        q = xb
+    else:
+        out = bd.try_fused_recurrent_attention_rope(xd, vd, dev(torch, rho0), dev(torch, dec),
+                                                    position=rope[0], chunk=chunk)
+        q = oracle.rope_rotate(xb, pos0=rope[0])
+    torch.cuda.synchronize()
+    assert out is not None
+    cref, rref = oracle.recurrent_f64(q, vb, rho0, dec)
+    e_ctx, e_rho = rel_l2(host(out.context), cref), rel_l2(host(out.rho), rref)
+    print(f"rel-L2 ctx {e_ctx:.2e} rho {e_rho:.2e}")
+    assert e_ctx <= TOL_BF16 and e_rho <= TOL_BF16
+
+
 def test_bf16_row_chunk_outside_the_abi_is_refused():
     torch = need_gpu()
     import burn_dragon_amd as bd
