@@ -42,6 +42,11 @@ class BdhLayerPlan(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in ("batch", "heads", "time", "latent", "embd")]
 
 
+class BdhLayerOptions(ctypes.Structure):
+    _fields_ = [("relu_threshold", ctypes.c_float), ("_pad", ctypes.c_int32),
+                ("latent_mask", ctypes.c_void_p)]
+
+
 class BdhLayerStateDesc(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int64), ("heads", ctypes.c_int64), ("latent", ctypes.c_int64),
                 ("embd", ctypes.c_int64), ("persist_sequence_state", ctypes.c_int32),
@@ -79,6 +84,9 @@ SIGNATURES = {
     "bdh_lowrank_pack_weights": (_i32, [_i64] * 3 + [_vp] * 7),
     "bdh_lowrank_layer_fwd": (_i32, [ctypes.POINTER(BdhLayerPlan), _vp, _vp, _vp, _vp,
                                      ctypes.POINTER(BdhRope), _vp, _vp, _vp, _vp]),
+    "bdh_lowrank_layer_fwd_ex": (_i32, [ctypes.POINTER(BdhLayerPlan), _vp, _vp, _vp, _vp,
+                                        ctypes.POINTER(BdhRope), _vp, _vp, _vp,
+                                        ctypes.POINTER(BdhLayerOptions), _vp]),
     "bdh_embed_norm": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
     "bdh_lm_head_pack": (_i32, [_i64, _i64, _vp, _vp, _vp]),
     "bdh_lm_logits": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),

@@ -2,6 +2,8 @@
 // with the reference's None semantics, path selection, per-device scratch,
 // the RoPE frequency table and the profiling counters.
 #include <math.h>
+
+#include <cmath>
 #include <string.h>
 
 #include <atomic>
@@ -612,7 +614,20 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
                                  const void* decoder_packed, const bdh_rope* rope,
                                  const float* rho_in, float* next_out, float* rho_out,
                                  void* stream) {
+  return bdh_lowrank_layer_fwd_ex(plan, current, encoder_packed, encoder_v_packed, decoder_packed, rope,
+                                  rho_in, next_out, rho_out, nullptr, stream);
+}
+
+bdh_status bdh_lowrank_layer_fwd_ex(const bdh_layer_plan* plan, const float* current,
+                                    const void* encoder_packed, const void* encoder_v_packed,
+                                    const void* decoder_packed, const bdh_rope* rope,
+                                    const float* rho_in, float* next_out, float* rho_out,
+                                    const bdh_layer_options* options, void* stream) {
   ProfScope prof;
+  if (options && !std::isfinite(options->relu_threshold))
+    return fail(BDH_EINVAL, "relu_threshold must be finite");
+  if (options && options->latent_mask && ((uintptr_t)options->latent_mask & 15) != 0)
+    return fail(BDH_EINVAL, "latent_mask must be 16-byte aligned");
   if (!plan) return fail(BDH_EINVAL, "null plan");
   bdh_recurrent_plan p{plan->batch, plan->heads, 1, plan->time, plan->latent, plan->embd};
   bdh_status st = check_plan(&p);
@@ -654,6 +669,8 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
   a.N = p.latent;
   a.D = p.embd;
   a.state_interval = state_interval(p.time, 0, false);  // layer attention has no decay
+  a.relu_th = options ? options->relu_threshold : 0.0f;
+  a.mask = options ? options->latent_mask : nullptr;
   st = run_layer(a, (hipStream_t)stream, &prof.launches);
   if (st == BDH_OK) prof.done(true);
   return st;

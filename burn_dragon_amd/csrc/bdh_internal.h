@@ -128,6 +128,8 @@ struct LayerArgs {
   float* rho_out;       // [B, H, N, D] or null; == rho_in with T = 1: sparse decode step
   int64_t B, H, T, N, D;
   int64_t state_interval;  // state-carry interval when rho_out is set
+  float relu_th = 0.0f;    // ReLU threshold of both projections
+  const float* mask = nullptr;  // latent mask [N] of both projections, or null
 };
 bool layer_shape_supported(int64_t N, int64_t D, const char** why);
 bdh_status pack_lowrank_weights(int64_t H, int64_t N, int64_t D, const float* enc,

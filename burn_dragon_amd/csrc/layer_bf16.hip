@@ -40,7 +40,14 @@ struct LayerGemmArgs {
   int64_t B, H, T, N, D, M;  // M = B * T
   int64_t V;          // L: vocabulary
   int mt, ct, ks;     // tiles along M and along the output columns; Z: K splits
+  float relu_th;      // X, Y: ReLU threshold (subtracted before the ReLU)
+  const float* mask;  // X, Y: latent mask [N] (times the ReLU), or null (ones)
 };
+
+// The activation of the reference's low-rank projection (relu_lowrank.rs
+// reference_forward, kernel/relu_lowrank.rs:100-135): subtract the
+// threshold, ReLU, times the latent mask.
+__device__ __forceinline__ float lowrank_act(float v, float th, float m) { return fmaxf(v - th, 0.0f) * m; }
 
 // One output tile.  Tile id -> (row tile, column tile, K split).  X and Y
 // (whose launches are mostly their [B, H, T, N] stores): column tiles
@@ -125,6 +132,9 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
     float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
     const int col = 8 * (lane & 15);
     const int64_t c = c0 + col, n = c - h * g.N;
+    float mk[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mk[j] = g.mask ? g.mask[n + j] : 1.0f;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
@@ -152,7 +162,8 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
         uint32_t yw[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          yw[j] = pack_bf16x2(fmaxf(a[2 * j], 0.0f) * bf16_lo(xw[j]), fmaxf(a[2 * j + 1], 0.0f) * bf16_hi(xw[j]));
+          yw[j] = pack_bf16x2(lowrank_act(a[2 * j], g.relu_th, mk[2 * j]) * bf16_lo(xw[j]),
+                              lowrank_act(a[2 * j + 1], g.relu_th, mk[2 * j + 1]) * bf16_hi(xw[j]));
         if (m0 + 64 * w + mi * 16 + row < g.M)
           *reinterpret_cast<uint4*>(dst[rr]) = make_uint4(yw[0], yw[1], yw[2], yw[3]);
       }
@@ -167,18 +178,23 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
     // lane's columns (pairs (n, n+1) .. (n+6, n+7)) are the same in every
     // call, so their frequencies are loaded once per tile.
     float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int64_t n0 = c0 + 8 * (lane & 15) - h * g.N;
     if (g.q) {
-      const int64_t n0 = c0 + 8 * (lane & 15) - h * g.N;
 #pragma unroll
       for (int j = 0; j < 4; ++j) fq[j] = g.freqs[n0 + 2 * j];
     }
+    float mk[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mk[j] = g.mask ? g.mask[n0 + j] : 1.0f;
     epilogue8_64x128(acc, lds, w, lane, [&](int row, int col, float4 lo, float4 hi) {
       const int64_t m = m0 + 64 * w + row, c = c0 + col;
       if (m >= g.M) return;
       const int64_t bb = m / g.T, t = m - bb * g.T, n = c - h * g.N;
       const int64_t o = ((bb * g.H + h) * g.T + t) * g.N + n;
-      const float r[8] = {fmaxf(lo.x, 0.0f), fmaxf(lo.y, 0.0f), fmaxf(lo.z, 0.0f), fmaxf(lo.w, 0.0f),
-                          fmaxf(hi.x, 0.0f), fmaxf(hi.y, 0.0f), fmaxf(hi.z, 0.0f), fmaxf(hi.w, 0.0f)};
+      const float th = g.relu_th;
+      const float r[8] = {lowrank_act(lo.x, th, mk[0]), lowrank_act(lo.y, th, mk[1]), lowrank_act(lo.z, th, mk[2]),
+                          lowrank_act(lo.w, th, mk[3]), lowrank_act(hi.x, th, mk[4]), lowrank_act(hi.y, th, mk[5]),
+                          lowrank_act(hi.z, th, mk[6]), lowrank_act(hi.w, th, mk[7])};
       __builtin_nontemporal_store(u32x4{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]),
                                         pack_bf16x2(r[4], r[5]), pack_bf16x2(r[6], r[7])},
                                   reinterpret_cast<u32x4*>(g.xy + o));
@@ -306,6 +322,7 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(LayerGemmArgs g) {
   }
   const int64_t c = c0 + (lane & 15);
   const int64_t n = c - h * g.N;
+  const float mk = (WAVECOL && g.mask) ? g.mask[n < g.N ? n : g.N - 1] : 1.0f;
   // Epilogue of the 16 x 16 block of row block mb (lane: rows
   // 4 (lane >> 4) + r, column lane & 15).
   auto emit = [&](int mb, const floatx4& v) {
@@ -315,7 +332,7 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(LayerGemmArgs g) {
       float val = v[r];
       if (KIND == G_X) {
         // Every lane joins the partner exchange before any row test.
-        const float x = fmaxf(val, 0.0f);
+        const float x = lowrank_act(val, g.relu_th, mk);
         const float xp = __shfl_xor(x, 1, 64);  // column c ^ 1 of the same row
         if (m >= g.M) continue;
         const int64_t bb = m / g.T, t = m - bb * g.T;
@@ -336,7 +353,7 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(LayerGemmArgs g) {
         if (KIND == G_Y) {
           const int64_t bb = m / g.T, t = m - bb * g.T;
           bf16_t* dst = g.xy + ((bb * g.H + h) * g.T + t) * g.N + n;
-          *dst = (bf16_t)(fmaxf(val, 0.0f) * (float)*dst);
+          *dst = (bf16_t)(lowrank_act(val, g.relu_th, mk) * (float)*dst);
         } else if (KIND == G_Z) {
           g.zpart[((int64_t)kp * g.M + m) * g.D + c] = val;
         } else if (c < g.V) {
@@ -701,6 +718,8 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   g.freqs = a.freqs;
   g.pos0 = a.pos0;
   g.fixed = a.fixed;
+  g.relu_th = a.relu_th;
+  g.mask = a.mask;
   BDH_HIP_TRY(launch_gemm<G_X>(g, st));
   g.q = nullptr;
   g.xf = nullptr;

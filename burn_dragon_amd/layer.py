@@ -1,11 +1,11 @@
 """Low-rank BDH layer body around the recurrent attention (bf16 MFMA, fp32
 accumulation): lowrank_residual_step_impl of
-crates/burn_dragon_core/src/model/residual_stream.rs:323-572 with its default
-options (no ReLU threshold, no sparse latent mask, dropout off):
+crates/burn_dragon_core/src/model/residual_stream.rs:323-572, dropout off,
+with its ReLU threshold th and sparse latent mask (default none):
 
-    x    = ReLU(cur E_h)                              [B, H, T, N]
+    x    = ReLU(cur E_h - th) * mask                  [B, H, T, N]
     a    = LN(recurrent_attention(rope(x), cur))      [B, H, T, D]
-    y    = ReLU(a Ev_h) * x
+    y    = (ReLU(a Ev_h - th) * mask) * x
     next = LN(cur + LN(y' Dec)),  y' = [B*T, H*N]      [B, T, D]
 
 LN is DragonNorm's LayerNorm arm (gamma 1, beta 0, eps 1e-5, biased
@@ -70,15 +70,20 @@ class LowRankLayerOutput(NamedTuple):
 def lowrank_layer_forward(current: torch.Tensor, weights: LowRankWeights, *,
                           position: Optional[int] = 0, theta: float = DEFAULT_ROPE_THETA,
                           want_rho: bool = False, out: Optional[torch.Tensor] = None,
-                          rho: Optional[torch.Tensor] = None, inplace: bool = False
+                          rho: Optional[torch.Tensor] = None, inplace: bool = False,
+                          relu_threshold: float = 0.0, latent_mask: Optional[torch.Tensor] = None
                           ) -> Optional[LowRankLayerOutput]:
     """current [B,1,T,D] or [B,T,D] f32 on the device; ``position`` is the
     first token's RoPE position (None: no rotation).  ``rho`` [B,H,N,D] f32
     is the layer's carried state (None: zeros).  With ``inplace`` the
     successor state is written over ``rho`` (the model's per-layer state;
     a single token then takes the sparse decode step); otherwise it is
-    returned in a new tensor when ``want_rho``.  Returns None where the
-    library does not support the shape."""
+    returned in a new tensor when ``want_rho``.  ``relu_threshold`` is the
+    config's relu_threshold (config.rs:64) and ``latent_mask`` the sparse
+    latent mask ([N] or the reference's [1,1,1,N] f32, e.g.
+    BlockPattern1d::mask), both applied in the two projections as
+    relu_lowrank.rs reference_forward does.  Returns None where the library
+    does not support the shape."""
     if not supports_backend() or weights is None:
         return None
     cur = current.reshape(current.shape[0], current.shape[-2], current.shape[-1])
@@ -105,14 +110,21 @@ def lowrank_layer_forward(current: torch.Tensor, weights: LowRankWeights, *,
         rho_out = torch.empty((B, H, N, D), device=cur.device, dtype=torch.float32)
     else:
         rho_out = None
+    mask = None
+    if latent_mask is not None:
+        mask = latent_mask.reshape(-1)
+        if mask.numel() != N or mask.dtype != torch.float32 or not mask.is_cuda:
+            return None
+        mask = mask.contiguous()
     plan = _lib.BdhLayerPlan(B, H, T, N, D)
     rope = None
     if position is not None:
         rope = _lib.BdhRope(_lib.BDH_ROPE_SEQUENTIAL, 0, int(position), float(theta))
-    st = _lib.load().bdh_lowrank_layer_fwd(
+    opts = _lib.BdhLayerOptions(float(relu_threshold), 0, _ptr(mask))
+    st = _lib.load().bdh_lowrank_layer_fwd_ex(
         ctypes.byref(plan), _ptr(cur), _ptr(weights.encoder), _ptr(weights.encoder_v),
         _ptr(weights.decoder), ctypes.byref(rope) if rope else None, _ptr(rho_in), _ptr(nxt),
-        _ptr(rho_out), ctypes.c_void_p(_stream_ptr(cur.device)))
+        _ptr(rho_out), ctypes.byref(opts), ctypes.c_void_p(_stream_ptr(cur.device)))
     if not _lib.check(st):
         return None
     return LowRankLayerOutput(nxt, rho_out)

@@ -81,11 +81,13 @@ def new_model_state(weights: BdhModelWeights, batch: int, device: torch.device,
 
 def model_forward_logits(tokens: torch.Tensor, weights: BdhModelWeights, *,
                          position: Optional[int] = 0, theta: float = DEFAULT_ROPE_THETA,
-                         state: Optional[BdhModelState] = None) -> Optional[torch.Tensor]:
+                         state: Optional[BdhModelState] = None, relu_threshold: float = 0.0,
+                         latent_mask: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
     """tokens [B, T] int32 on the device -> logits [B, T, vocab] f32.
     Without ``state`` every layer starts from rho = 0 at ``position``; with
     it the forward continues the state's sequence (its position wins) and
-    updates the state in place."""
+    updates the state in place.  ``relu_threshold`` and ``latent_mask`` are
+    every layer's projection options (lowrank_layer_forward)."""
     if not supports_backend() or weights is None:
         return None
     if state is not None:
@@ -109,7 +111,8 @@ def model_forward_logits(tokens: torch.Tensor, weights: BdhModelWeights, *,
     for layer in range(weights.n_layer):
         rho = state.rho[layer] if state is not None else None
         out = lowrank_layer_forward(cur, weights.layer, position=position, theta=theta, out=nxt,
-                                    rho=rho, inplace=state is not None)
+                                    rho=rho, inplace=state is not None,
+                                    relu_threshold=relu_threshold, latent_mask=latent_mask)
         if out is None:
             return None
         cur, nxt = nxt, cur

@@ -211,11 +211,12 @@ bdh_status bdh_recurrent_attention_vjp(const bdh_recurrent_plan* plan, const flo
 
 /* Low-rank BDH layer body around the recurrent attention, bf16 MFMA with
  * fp32 accumulation.  Replaces lowrank_residual_step_impl
- * (crates/burn_dragon_core/src/model/residual_stream.rs:323-572) with its
- * default options (no ReLU threshold, no sparse latent mask, dropout off):
- *   x    = ReLU(cur E_h)                       per head h, [B,H,T,N]
+ * (crates/burn_dragon_core/src/model/residual_stream.rs:323-572), dropout
+ * off; bdh_lowrank_layer_fwd takes its default options (no ReLU threshold,
+ * no sparse latent mask), bdh_lowrank_layer_fwd_ex the options below:
+ *   x    = ReLU(cur E_h - th) * mask            per head h, [B,H,T,N]
  *   a    = LN(attention(rope(x), value = cur))  (sequence_dispatch.rs:83-136)
- *   y    = ReLU(a Ev_h) * x
+ *   y    = (ReLU(a Ev_h - th) * mask) * x
  *   next = LN(cur + LN(decode_y_neuron_tail(y, Dec)))   (:309-321)
  * LN = DragonNorm LayerNorm with gamma = 1, beta = 0, eps = 1e-5 (norm.rs:302-328).
  * current, next_out [B,T,D] f32 (Burn's [B,1,T,D]); weights packed by
@@ -250,6 +251,32 @@ bdh_status bdh_lowrank_layer_fwd(const bdh_layer_plan* plan, const float* curren
                                  const void* decoder_packed, const bdh_rope* rope,
                                  const float* rho_in, float* next_out, float* rho_out,
                                  void* stream);
+
+/* Options of the layer's two low-rank projections, as the fused projection
+ * of the reference applies them (relu_lowrank.rs reference_forward,
+ * crates/burn_dragon_core/src/kernel/relu_lowrank.rs:100-135, called with
+ * the layer's threshold and mask at residual_stream.rs:377-410, 440-470):
+ *   relu_threshold  FusedKernelConfig::relu_threshold (config.rs:64): th,
+ *                   subtracted before the ReLU (0 = none);
+ *   latent_mask     [latent] f32 device pointer, 16-byte aligned, or NULL:
+ *                   the sparse latent mask (BlockPattern1d::mask,
+ *                   block_sparse.rs:49-64: 1 on active blocks, 0 elsewhere;
+ *                   any values are applied as given), shared by the heads.
+ * The layer passes no bias to its projections, so there is none here. */
+typedef struct {
+  float relu_threshold;
+  int32_t _pad;
+  const float* latent_mask;
+} bdh_layer_options;
+
+/* bdh_lowrank_layer_fwd with options (NULL = the defaults).  Same
+ * arguments otherwise; a non-finite threshold or a misaligned mask is
+ * BDH_EINVAL. */
+bdh_status bdh_lowrank_layer_fwd_ex(const bdh_layer_plan* plan, const float* current,
+                                    const void* encoder_packed, const void* encoder_v_packed,
+                                    const void* decoder_packed, const bdh_rope* rope,
+                                    const float* rho_in, float* next_out, float* rho_out,
+                                    const bdh_layer_options* options, void* stream);
 
 /* The model's input: out = LN(embed[token]) per token, the embedding lookup
  * followed by DragonModel's input norm (dragon.rs:3352, norm.rs:302-328).

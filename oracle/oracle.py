@@ -223,33 +223,55 @@ def decode_y_neuron_tail_f64(y, decoder) -> np.ndarray:
 
 
 def lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=0, theta: float = 65536.0,
-                      rho0=None):
-    """lowrank_residual_step_impl (residual_stream.rs:323-572) with its
-    default options (no ReLU threshold, no sparse latent mask, dropout off):
-      x = ReLU(cur @ E_h)                                  (:377-395)
+                      rho0=None, relu_threshold: float = 0.0, latent_mask=None):
+    """lowrank_residual_step_impl (residual_stream.rs:323-572), dropout off,
+    with its ReLU threshold and sparse latent mask (relu_lowrank.rs
+    reference_forward, kernel/relu_lowrank.rs:100-135: project, subtract the
+    threshold, ReLU, times the mask; the layer passes no bias, :387-400,
+    :443-456):
+      x = ReLU(cur @ E_h - th) * mask                      (:377-410)
       attn = recurrent attention of rope(x) with value cur  (:398;
              sequence_dispatch.rs:97-111; linear.rs:18-60)
       attn = LN(attn)                                      (:422)
-      y = x * ReLU(attn @ Ev_h)                            (:440-486)
+      y = x * (ReLU(attn @ Ev_h - th) * mask)              (:440-486)
       mlp = LN(decode_y_neuron_tail(y, Dec))               (:488, :499)
       next = LN(cur + mlp)                                 (:517)
-    cur [B,T,D]; encoder, encoder_v [H,D,N]; decoder [H*N,D]; pos0 None = no
-    RoPE.  RoPE runs in the reference's f32 op order, everything else in f64.
-    Returns (next [B,T,D], rho [B,H,N,D])."""
+    cur [B,T,D]; encoder, encoder_v [H,D,N]; decoder [H*N,D]; latent_mask
+    [N] (BlockPattern1d::mask, block_sparse.rs:49-64, or any [N] mask) or
+    None; pos0 None = no RoPE.  RoPE runs in the reference's f32 op order,
+    everything else in f64.  Returns (next [B,T,D], rho [B,H,N,D])."""
     cur = np.asarray(cur, np.float64)
     enc = np.asarray(encoder, np.float64)
     encv = np.asarray(encoder_v, np.float64)
-    x = np.maximum(np.matmul(cur[:, None], enc[None]), 0.0)  # [B,H,T,N]
+    mask = None if latent_mask is None else np.asarray(latent_mask, np.float64)
+    x = np.maximum(np.matmul(cur[:, None], enc[None]) - relu_threshold, 0.0)  # [B,H,T,N]
+    if mask is not None:
+        x = x * mask
     q = rope_rotate(x.astype(np.float32), pos0=pos0, theta=theta) if pos0 is not None else x
     ctx, rho = recurrent_f64(q, cur[:, None].astype(np.float32), rho0)
     a = layer_norm_f64(ctx)
-    y = x * np.maximum(np.matmul(a, encv[None]), 0.0)
+    gate = np.maximum(np.matmul(a, encv[None]) - relu_threshold, 0.0)
+    if mask is not None:
+        gate = gate * mask
+    y = x * gate
     mlp = layer_norm_f64(decode_y_neuron_tail_f64(y, decoder))
     return layer_norm_f64(cur + mlp), rho
 
 
+def block_pattern_mask(latent: int, block_size: int, active_blocks=None) -> np.ndarray:
+    """BlockPattern1d::mask (kernel/block_sparse.rs:49-64): 1 on the active
+    blocks of block_size latents (all when active_blocks is None), else 0."""
+    m = np.zeros(latent, np.float32)
+    bs = max(1, block_size)
+    for blk in range((latent + bs - 1) // bs):
+        if active_blocks is None or blk in active_blocks:
+            m[blk * bs:min(latent, (blk + 1) * bs)] = 1.0
+    return m
+
+
 def model_forward_f64(tokens, embed, encoder, encoder_v, decoder, lm_head, n_layer: int,
-                      pos0=0, theta: float = 65536.0, rho0s=None, return_state: bool = False):
+                      pos0=0, theta: float = 65536.0, rho0s=None, return_state: bool = False,
+                      relu_threshold: float = 0.0, latent_mask=None):
     """DragonModel sequence forward with shared low-rank weights and the
     vanilla residual connector (dragon.rs:3340-3420): current =
     LN(embed[tokens]) (:3352), n_layer x lowrank_layer_f64 with the same
@@ -257,14 +279,16 @@ def model_forward_f64(tokens, embed, encoder, encoder_v, decoder, lm_head, n_lay
     :4033-4055).  tokens [B,T]; returns logits [B,T,vocab] f64.
     rho0s: per-layer carried states (each layer's LayerState.rho,
     dragon.rs:3437-3446), None = zeros; with return_state the per-layer
-    successor states are returned too."""
+    successor states are returned too.  relu_threshold and latent_mask go to
+    every layer."""
     emb = np.asarray(embed, np.float64)
     cur = layer_norm_f64(emb[np.asarray(tokens)])
     rhos = []
     for layer in range(n_layer):
         rho0 = rho0s[layer] if rho0s is not None else None
         cur, rho = lowrank_layer_f64(cur, encoder, encoder_v, decoder, pos0=pos0, theta=theta,
-                                     rho0=rho0)
+                                     rho0=rho0, relu_threshold=relu_threshold,
+                                     latent_mask=latent_mask)
         rhos.append(rho)
     logits = cur @ np.asarray(lm_head, np.float64)
     return (logits, rhos) if return_state else logits

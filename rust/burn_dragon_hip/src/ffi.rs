@@ -55,6 +55,14 @@ pub struct bdh_layer_plan {
 }
 
 #[repr(C)]
+#[derive(Clone, Copy, Debug)]
+pub struct bdh_layer_options {
+    pub relu_threshold: f32,
+    pub _pad: i32,
+    pub latent_mask: *const f32,
+}
+
+#[repr(C)]
 #[derive(Clone, Copy, Debug, Default)]
 pub struct bdh_layer_state_desc {
     pub batch: i64,
@@ -130,6 +138,11 @@ extern "C" {
                                  decoder_packed: *const c_void, rope: *const bdh_rope,
                                  rho_in: *const f32, next_out: *mut f32, rho_out: *mut f32,
                                  stream: *mut c_void) -> i32;
+    pub fn bdh_lowrank_layer_fwd_ex(plan: *const bdh_layer_plan, current: *const f32,
+                                    encoder_packed: *const c_void, encoder_v_packed: *const c_void,
+                                    decoder_packed: *const c_void, rope: *const bdh_rope,
+                                    rho_in: *const f32, next_out: *mut f32, rho_out: *mut f32,
+                                    options: *const bdh_layer_options, stream: *mut c_void) -> i32;
     pub fn bdh_embed_norm(tokens: *const i32, n_tokens: i64, embed: *const f32, vocab: i64,
                           embd: i64, out: *mut f32, stream: *mut c_void) -> i32;
     pub fn bdh_lm_head_pack(embd: i64, vocab: i64, lm_head: *const f32, packed: *mut c_void,

@@ -216,3 +216,69 @@ def test_model_prompt_then_decode_matches_oracle(oracle):
     e_all, e_steps = rel_l2(got, ref), rel_l2(got[:, T0:], ref[:, T0:])
     print(f"rel-L2 logits {e_all:.2e}, decoded tokens {e_steps:.2e}")
     assert e_all <= TOL_BF16 and e_steps <= TOL_BF16
+
+
+@pytest.mark.parametrize("B,H,T,N,D,pos,mode,mask_kind", [
+    (1, 2, 300, 512, 128, 3, "copy", "blocks"),     # 256 x 128 tiles, block-sparse latent mask
+    (2, 2, 24, 256, 64, 5, "copy", "values"),       # few-row GEMMs, a mask of other values
+    (3, 2, 1, 512, 128, 9, "inplace", "blocks"),    # one token in place: the sparse decode step
+    (1, 2, 640, 256, 256, 0, "copy", None),         # the threshold alone, two state intervals
+])
+def test_layer_threshold_and_mask_match_oracle(oracle, B, H, T, N, D, pos, mode, mask_kind):
+    # relu_threshold and the sparse latent mask in both projections
+    # (relu_lowrank.rs reference_forward; residual_stream.rs:377-470) against
+    # the oracle pinned by scalar loops in tests/test_oracle_layer.py.
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    rng = np.random.default_rng(B * 300 + T + N + D)
+    cur, enc, encv, dec = _case(rng, B, H, T, N, D)
+    rho0 = (rng.standard_normal((B, H, N, D)) * 0.05).astype(np.float32)
+    th = 0.4
+    if mask_kind == "blocks":
+        mask = oracle.block_pattern_mask(N, 64, {b for b in range(N // 64) if b % 3 != 1})
+    elif mask_kind == "values":
+        mask = rng.choice([0.0, 0.5, 1.0, 1.5], N).astype(np.float32)
+    else:
+        mask = None
+    w = bd.LowRankWeights.pack(dev(torch, enc[None]), dev(torch, encv[None]), dev(torch, dec))
+    rho_t = dev(torch, rho0)
+    announce("layer threshold mask", B, H, T, N, D, pos, mode, mask_kind)
+    out = bd.lowrank_layer_forward(dev(torch, cur), w, position=pos, rho=rho_t,
+                                   inplace=mode == "inplace", want_rho=mode == "copy",
+                                   relu_threshold=th,
+                                   latent_mask=None if mask is None else dev(torch, mask[None, None, None]))
+    torch.cuda.synchronize()
+    assert out is not None
+    nref, rref = oracle.lowrank_layer_f64(cur, oracle.round_bf16(enc), oracle.round_bf16(encv),
+                                          oracle.round_bf16(dec), pos0=pos, rho0=rho0,
+                                          relu_threshold=th, latent_mask=mask)
+    plain, _ = oracle.lowrank_layer_f64(cur, oracle.round_bf16(enc), oracle.round_bf16(encv),
+                                        oracle.round_bf16(dec), pos0=pos, rho0=rho0)
+    e_next, e_rho = rel_l2(host(out.next), nref), rel_l2(host(out.rho), rref)
+    print(f"rel-L2 next {e_next:.2e} rho {e_rho:.2e} (vs the unmasked layer "
+          f"{rel_l2(nref, plain):.2e})")
+    assert rel_l2(nref, plain) > 5 * TOL_BF16  # the options change the output
+    assert e_next <= TOL_BF16 and e_rho <= TOL_BF16
+
+
+def test_layer_options_are_validated():
+    import ctypes
+    torch = need_gpu()
+    import burn_dragon_amd as bd
+    from burn_dragon_amd import _lib
+    rng = np.random.default_rng(3)
+    cur, enc, encv, dec = _case(rng, 1, 1, 16, 256, 64)
+    w = bd.LowRankWeights.pack(dev(torch, enc[None]), dev(torch, encv[None]), dev(torch, dec))
+    c, nxt = dev(torch, cur), torch.empty(1, 16, 64, device="cuda")
+    mask = torch.ones(257, device="cuda")
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    plan = _lib.BdhLayerPlan(1, 1, 16, 256, 64)
+    announce("layer options refused")
+    for th, m in ((float("nan"), None), (0.0, ctypes.c_void_p(mask.data_ptr() + 4))):
+        opts = _lib.BdhLayerOptions(th, 0, m)
+        st = _lib.load().bdh_lowrank_layer_fwd_ex(ctypes.byref(plan), p(c), p(w.encoder), p(w.encoder_v),
+                                                   p(w.decoder), None, None, p(nxt), None,
+                                                   ctypes.byref(opts), None)
+        assert st == _lib.BDH_EINVAL
+    # a wrongly sized mask is refused by the wrapper (the reference's None)
+    assert bd.lowrank_layer_forward(c, w, latent_mask=mask) is None

@@ -57,13 +57,25 @@ def _rope_list(xs, pos, theta=65536.0):
     return out
 
 
-def _layer_loops(cur, enc, encv, dec, pos0, bad=None):
+def _act(v, th, m, bad, where):
+    # relu_lowrank reference_forward on one scalar: (v - th), ReLU, times m
+    if bad == "threshold_after_relu":
+        return (max(0.0, v) - th) * m
+    if bad == "mask_before_relu":
+        return max(0.0, v * m - th)
+    if bad == "mask_only_x" and where == "y":
+        return max(0.0, v - th)
+    return max(0.0, v - th) * m
+
+
+def _layer_loops(cur, enc, encv, dec, pos0, bad=None, th=0.0, mask=None):
     B, T, D = cur.shape
     H, _, N = enc.shape
+    mk = [1.0] * N if mask is None else [float(v) for v in mask]
     nxt = np.zeros((B, T, D))
     for b in range(B):
-        x = [[[max(0.0, sum(cur[b, t, d] * enc[h, d, n] for d in range(D))) for n in range(N)]
-              for t in range(T)] for h in range(H)]
+        x = [[[_act(sum(cur[b, t, d] * enc[h, d, n] for d in range(D)), th, mk[n], bad, "x")
+               for n in range(N)] for t in range(T)] for h in range(H)]
         attn = [[None] * T for _ in range(H)]
         for h in range(H):
             rho = [[0.0] * D for _ in range(N)]
@@ -84,7 +96,7 @@ def _layer_loops(cur, enc, encv, dec, pos0, bad=None):
                 a = attn[h][t] if bad == "no_attn_norm" else _ln_list(attn[h][t])
                 for n in range(N):
                     g = sum(a[d] * encv[h, d, n] for d in range(D))
-                    yv = x[h][t][n] * (g if bad == "gate_without_relu" else max(0.0, g))
+                    yv = x[h][t][n] * (g if bad == "gate_without_relu" else _act(g, th, mk[n], bad, "y"))
                     for d in range(D):
                         z[d] += yv * dec[h * N + n, d]
             mlp = z if bad == "no_mlp_norm" else _ln_list(z)
@@ -105,6 +117,36 @@ def test_layer_matches_scalar_loops_and_catches_planted_mistakes(oracle):
     for bad in ("update_before_read", "no_attn_norm", "gate_without_relu", "no_mlp_norm"):
         wrong = _layer_loops(cur, enc, encv, dec, 3, bad=bad)
         assert np.max(np.abs(got - wrong)) > 1e-3, bad
+
+
+def test_layer_threshold_and_mask_match_scalar_loops(oracle):
+    # The ReLU threshold and the latent mask (relu_lowrank.rs reference_forward:
+    # subtract, ReLU, times the mask, in both projections): a threshold inside
+    # the projections' range and a mask with values other than 0 and 1, so
+    # that each plausible misplacement changes the output.
+    rng = np.random.default_rng(21)
+    B, T, D, H, N = 1, 4, 4, 2, 4
+    cur = rng.standard_normal((B, T, D))
+    enc = rng.standard_normal((H, D, N)) * 0.7
+    encv = rng.standard_normal((H, D, N)) * 0.7
+    dec = rng.standard_normal((H * N, D)) * 0.5
+    th, mask = 0.3, np.array([1.0, 0.5, 0.0, 2.0])
+    got, _ = oracle.lowrank_layer_f64(cur, enc, encv, dec, pos0=3, relu_threshold=th, latent_mask=mask)
+    ref = _layer_loops(cur, enc, encv, dec, 3, th=th, mask=mask)
+    assert np.max(np.abs(got - ref)) < 1e-5
+    plain, _ = oracle.lowrank_layer_f64(cur, enc, encv, dec, pos0=3)
+    assert np.max(np.abs(got - plain)) > 1e-3
+    for bad in ("threshold_after_relu", "mask_before_relu", "mask_only_x"):
+        wrong = _layer_loops(cur, enc, encv, dec, 3, bad=bad, th=th, mask=mask)
+        assert np.max(np.abs(got - wrong)) > 1e-3, bad
+
+
+def test_block_pattern_mask(oracle):
+    # BlockPattern1d::mask (block_sparse.rs:49-64): whole blocks, the last one
+    # ragged; dense when no blocks are listed.
+    m = oracle.block_pattern_mask(10, 4, {0, 2})
+    assert m.tolist() == [1, 1, 1, 1, 0, 0, 0, 0, 1, 1]
+    assert oracle.block_pattern_mask(5, 2).tolist() == [1] * 5
 
 
 def test_model_oracle_composition(oracle):

@@ -56,6 +56,10 @@ def header_structs():
             decl = " ".join(decl.split())
             if not decl:
                 continue
+            if "*" in decl or decl.startswith("const "):
+                mm = re.match(r"(.*?)(\w+)$", decl)  # one pointer field: "const float* name"
+                fields.append((mm.group(2), c_to_rust(mm.group(1))))
+                continue
             typ, names = decl.split(" ", 1)
             for n in names.split(","):
                 fields.append((n.strip(), SCALARS.get(typ, typ)))
