@@ -41,8 +41,8 @@ SEED = 20260729
 TRAFFIC_PREFILL_C2 = 1098.4e6       # one prefill_mfma_kernel launch
 TRAFFIC_PREFILL_C2_PASS = 1165.7e6  # the whole C2 pass (transpose_v, prefill, ctx)
 TRAFFIC_DECODE_C3 = 428.0e6         # one decode_kernel launch
-TRAFFIC_LONG_C4 = 2659.0e6          # the carry and snap_wide launches of one C4 call (row chunk 512)
-TRAFFIC_LONG_C4_CALL = 2856.5e6     # the whole C4 call
+TRAFFIC_LONG_C4 = 2637.0e6          # the carry and snap_wide launches of one C4 call (row chunk 512)
+TRAFFIC_LONG_C4_CALL = 2834.5e6     # the whole C4 call
 
 
 def parse():
