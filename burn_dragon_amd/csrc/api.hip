@@ -600,6 +600,7 @@ bdh_status bdh_lowrank_pack_weights(int64_t heads, int64_t latent, int64_t embd,
     return fail(BDH_EINVAL, "null tensor pointer");
   if (heads * latent > (int64_t)32 * kMaxGrid) return fail(BDH_UNSUPPORTED, "heads * latent too large");
   if (heads > kMaxGrid) return fail(BDH_UNSUPPORTED, "heads exceeds 65535");
+  if ((heads * latent) % 128 != 0) return fail(BDH_UNSUPPORTED, "heads * latent must be a multiple of 128");
   bdh_status st = pack_lowrank_weights(heads, latent, embd, encoder, encoder_v, decoder,
                                        (bf16_t*)encoder_packed, (bf16_t*)encoder_v_packed,
                                        (bf16_t*)decoder_packed, (hipStream_t)stream);

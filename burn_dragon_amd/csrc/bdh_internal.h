@@ -119,7 +119,7 @@ struct LayerArgs {
   const float* cur;     // [B, T, D]
   const bf16_t* enc;    // packed encoder   [H, N, D]
   const bf16_t* encv;   // packed encoder_v [H, N, D]
-  const bf16_t* dec;    // packed decoder   [D, H*N]
+  const bf16_t* dec;    // packed decoder   [H*N/128, D, 128] (chunk-major)
   const float* freqs;   // device RoPE frequencies or null
   int64_t pos0;
   int fixed;

@@ -161,6 +161,17 @@ __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t
                "{m0}"(m0)
                : "memory");
 }
+// As dma16 with the non-temporal hint: for data read once, so that it does
+// not evict the L2 lines of operands that are read again.
+__device__ __forceinline__ void dma16_nt(const void* gbase, uint32_t voff, uint32_t m0) {
+  const uint64_t b = reinterpret_cast<uint64_t>(gbase);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t bu = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(reinterpret_cast<const void*>(bu)),
+               "{m0}"(m0)
+               : "memory");
+}
 // As dma16 with 4 bytes per lane, written to LDS at m0 + 4 * lane.
 __device__ __forceinline__ void dma4(const void* gbase, uint32_t voff, uint32_t m0) {
   const uint64_t b = reinterpret_cast<uint64_t>(gbase);
@@ -224,6 +235,37 @@ __device__ __forceinline__ void mma_64x128_dsasm(const bf16_t* A, const bf16_t* 
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
     for (int ni = 4; ni < 8; ++ni) mm(mi, ni);
+}
+
+// The same for a 64 x 64 block: 4 A and 4 B fragments, 16 MFMAs;
+// acc[mi][ni] += A[arow + 16 mi] x B[brow + 16 ni]^T.
+__device__ __forceinline__ void mma_64x64_dsasm(const bf16_t* A, const bf16_t* B, int lane, int arow,
+                                                int brow, floatx4 (&acc)[4][4]) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  const uint32_t a = lds_addr(A) + (uint32_t)(2 * lds_off(arow + (lane & 15), lane >> 4));
+  const uint32_t b = lds_addr(B) + (uint32_t)(2 * lds_off(brow + (lane & 15), lane >> 4));
+  u32x4_t af[4], bf[4];
+#define BDH_DSR(dst, addr, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "n"(off))
+  BDH_DSR(af[0], a, 0);
+  BDH_DSR(bf[0], b, 0);
+  BDH_DSR(bf[1], b, 1024);
+  BDH_DSR(bf[2], b, 2048);
+  BDH_DSR(bf[3], b, 3072);
+  BDH_DSR(af[1], a, 1024);
+  BDH_DSR(af[2], a, 2048);
+  BDH_DSR(af[3], a, 3072);
+#undef BDH_DSR
+  auto mm = [&](int mi, int ni) {
+    acc[mi][ni] = mfma16(__builtin_bit_cast(bf16x8, af[mi]), __builtin_bit_cast(bf16x8, bf[ni]), acc[mi][ni]);
+  };
+  asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(af[0]), "+v"(bf[0]), "+v"(bf[1]), "+v"(bf[2]), "+v"(bf[3]));
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) mm(0, ni);
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[1]), "+v"(af[2]), "+v"(af[3]));
+#pragma unroll
+  for (int mi = 1; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) mm(mi, ni);
 }
 
 // Cross-step form of mma_64x128_dsasm for rings whose next stage is known to

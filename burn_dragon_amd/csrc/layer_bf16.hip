@@ -6,7 +6,10 @@
 //                                                         writes q = rope(x))
 //   a    = LN(attn(q, v = cur))          [B, H, T, D]   (prefill_bf16.hip, ln_rows)
 //   y    = ReLU(a Ev_h) * x              [B, H, T, N]   (GEMM Y, written over x)
-//   z    = y' Dec, y' = [B*T, H*N]       [B, T, D]      (GEMM Z, split-K partials)
+//   z    = y' Dec, y' = [B*T, H*N]       [B, T, D]      (GEMM Z, split-K partials;
+//                                                         with T % 256 == 0 and D <= 256
+//                                                         one launch computes y tile by
+//                                                         tile and never stores it)
 //   next = LN(cur + LN(z))               [B, T, D]      (residual_kernel)
 //
 // LN is DragonNorm's LayerNorm arm with gamma = 1, beta = 0, eps = 1e-5 and
@@ -23,6 +26,16 @@ namespace {
 using namespace mfma;
 
 enum { G_X = 0, G_Y = 1, G_Z = 2, G_L = 3 };
+
+// The packed decoder is chunk-major, [H N / 128, D, 128]: the transpose
+// [D, H N] cut into 128-latent chunks, each a contiguous 64 KiB block at
+// D = 256.  The decoder products read one 32-latent step of D rows at a
+// time: with the plain transpose those rows lie 64 KiB apart (C5), the same
+// L2 sets for every row, and the fused Y + Z launch fetched 3.8 GB past L2
+// for 1.1 GB of operands.  Element (d, k) of the transpose:
+__host__ __device__ constexpr int64_t dec_off(int64_t d, int64_t k, int64_t D) {
+  return (k / 128) * D * 128 + d * 128 + (k % 128);
+}
 
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
@@ -42,6 +55,7 @@ struct LayerGemmArgs {
   int mt, ct, ks;     // tiles along M and along the output columns; Z: K splits
   float relu_th;      // X, Y: ReLU threshold (subtracted before the ReLU)
   const float* mask;  // X, Y: latent mask [N] (times the ReLU), or null (ones)
+  const bf16_t* dec;  // Y fused into Z (layer_yz_kernel): decoder [D, H*N]
 };
 
 // The activation of the reference's low-rank projection (relu_lowrank.rs
@@ -98,7 +112,7 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
   for (int gi = 0; gi < 2; ++gi) {
     int64_t c = c0 + rb + 64 * gi;
     c = c < ncols ? c : ncols - 1;
-    brow[gi] = g.b + c * K + kc * 8;
+    brow[gi] = g.b + (KIND == G_Z ? c * 128 : c * K) + kc * 8;
   }
   uint4 st[6];
   auto load = [&](int kt) {
@@ -108,7 +122,7 @@ __device__ __forceinline__ void gemm_tile(const LayerGemmArgs& g, bf16_t* lds, i
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) st[gi] = ldg16(arow[gi] + aoff);
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) st[4 + gi] = ldg16(brow[gi] + k0);
+    for (int gi = 0; gi < 2; ++gi) st[4 + gi] = ldg16(brow[gi] + (KIND == G_Z ? dec_off(0, k0, g.D) : k0));
   };
   auto store = [&](int buf) {
     bf16_t* base = lds + buf * BUF;  // A rows 0..255, then B rows 256..383
@@ -251,6 +265,268 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
   for (int id = blockIdx.x; id < total; id += gridDim.x) gemm_tile<KIND>(g, lds, id);
 }
 
+// ---- GEMM Y fused into GEMM Z --------------------------------------------
+// With T a multiple of 256 and D <= 256 the layer never writes y.  One
+// workgroup (8 waves, one per CU) owns a 256-token tile (one sequence) and a
+// range of 128-latent chunks of H N, and per chunk
+//   Y^T  = Ev_chunk a_h^T        [128 latents x 256 tokens], K = D
+//   y    = act(Y) * x            bf16, into LDS as the next product's A operand
+//   z   += y Dec_chunk^T         [256 tokens x D], K = 128
+// with z in the accumulators across the chunks, written at the end as the
+// split-K partial [kp, M, D] that the residual kernel sums in order.  Y is
+// computed transposed so that each accumulator register of a lane holds 4
+// consecutive latents of one token: one 8-byte read of x and one 8-byte
+// write of y.  y is rounded to bf16 exactly as GEMM Y stores it.
+// Operands stream through a 3-slot direct-load ring two steps ahead (a step
+// is 32 deep: a Y step loads 256 a_h rows and 128 Ev rows, a z step 256
+// decoder rows); x lands in the y buffer itself, in pairs of 32-latent
+// blocks as soon as the previous chunk's z steps have read them.  (A 4-slot ring, three
+// steps ahead in all 160 KiB of LDS, was slower: C5 1.08 against 0.98 ms
+// per launch.)
+constexpr int YZ_C = T256 / 2;  // latents per chunk
+constexpr int YZ_RING = 3;
+constexpr int YZ_PREF = YZ_RING - 1;  // steps loaded ahead
+
+// Tile geometry of the launch with NW waves: TM = 32 NW tokens.
+template <int NW>
+struct YZGeom {
+  static constexpr int NT = 64 * NW;
+  static constexpr int TM = 32 * NW;                   // token rows of the tile
+  static constexpr int SLOT = (TM + YZ_C) * BK * 2;    // ring slot: a_h rows, then Ev rows (z: decoder rows)
+  static constexpr int KB = TM * BK * 2;               // one 32-latent block of y
+  static constexpr int YBUF = YZ_RING * SLOT;
+  static constexpr int LDS = YBUF + 4 * KB;
+  static constexpr int YDMA = (TM / 16 + 8) / NW;      // DMAs a wave issues per Y stage
+  static constexpr int ZDMA = 16 / NW;                 // per z stage (256 decoder rows)
+  static constexpr int XDMA = TM / 16 / NW;            // per 32-latent x block
+};
+
+// Wait until at most n of this wave's DMAs are in flight, then a barrier.
+__device__ __forceinline__ void yz_wait_barrier(int n) {
+  switch (n) {
+    case 1: dma_wait_barrier<1>(); break;
+    case 2: dma_wait_barrier<2>(); break;
+    case 3: dma_wait_barrier<3>(); break;
+    case 4: dma_wait_barrier<4>(); break;
+    case 5: dma_wait_barrier<5>(); break;
+    case 6: dma_wait_barrier<6>(); break;
+    case 7: dma_wait_barrier<7>(); break;
+    case 8: dma_wait_barrier<8>(); break;
+    default: dma_wait_barrier<0>(); break;
+  }
+}
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void layer_yz_kernel(LayerGemmArgs g) {
+  using Geo = YZGeom<NW>;
+  constexpr int TM = Geo::TM;
+  __shared__ __attribute__((aligned(16))) char lds[Geo::LDS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // Workgroup id i runs on XCD i % 8.  With 8 | mt an XCD takes mt / 8
+  // token tiles with all ks latent ranges: its L2 then holds those tiles'
+  // a_h rows (re-read at every chunk) and the ks chunks' weights being
+  // streamed (C5: 1 MB + 512 KB).  Giving an XCD one latent range and 32
+  // token tiles instead put 4 MB of a_h rows on its 4 MB L2.
+  const int id = (int)blockIdx.x;
+  int kp, mtile;
+  if (g.mt % 8 == 0) {
+    const int slot = id >> 3;
+    mtile = (id & 7) * (g.mt >> 3) + slot / g.ks;
+    kp = slot % g.ks;
+  } else {
+    kp = id / g.mt;
+    mtile = id - kp * g.mt;
+  }
+  const int64_t HN = g.H * g.N;
+  const int nc = (int)(HN / YZ_C), cpn = (int)(g.N / YZ_C);  // chunks, chunks per head
+  const int jb = (int)((int64_t)nc * kp / g.ks), je = (int)((int64_t)nc * (kp + 1) / g.ks);
+  const int ny = (int)(g.D / BK), per = ny + 4;  // Y steps, then 4 z steps, per chunk
+  const int64_t m0 = (int64_t)mtile * TM, bb = m0 / g.T, t0 = m0 - bb * g.T;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  // DMA lanes (16 rows of 64 bytes per instruction): the lane writing slot
+  // c of row r fetches chunk c ^ ((r >> 1) & 3), the swizzle of lds_off.
+  // Block b of 16 rows goes to wave b % NW.
+  const uint32_t gc16 = (uint32_t)(((lane & 3) ^ ((lane >> 3) & 3)) * 16);
+  const uint32_t rsub = (uint32_t)(lane >> 2);
+  const uint32_t rowA = (uint32_t)(g.D * 2), rowX = (uint32_t)(g.N * 2), rowDec = YZ_C * 2;  // row pitches, bytes
+  // Per-lane offsets of the wave's first row (16 w + rsub); the wave's
+  // further blocks, 16 NW rows on each, go through the (uniform) base.
+  const uint32_t offA = (16 * w + rsub) * rowA + gc16, offX = (16 * w + rsub) * rowX + gc16;
+  const int64_t stepA = 16 * NW * (int64_t)rowA, stepX = 16 * NW * (int64_t)rowX;
+  uint32_t offD[Geo::ZDMA];  // decoder rows, clamped to D - 1
+#pragma unroll
+  for (int i = 0; i < Geo::ZDMA; ++i) {
+    const uint32_t d = 16 * (w + NW * i) + rsub;
+    offD[i] = (d < (uint32_t)g.D ? d : (uint32_t)g.D - 1) * rowDec + gc16;
+  }
+
+  // Operand bases of chunk j (one division per chunk, none per step).
+  struct Bases {
+    const char* A;   // a_h rows of the token tile, head of the chunk
+    const char* E;   // Ev rows of the chunk
+    const char* Dc;  // the chunk's decoder block [D, 128]
+    const char* X;   // x rows of the token tile at the chunk's first latent
+    int64_t n0;      // first latent of the chunk in its head
+  };
+  auto bases = [&](int j) {
+    Bases c;
+    const int64_t h = j / cpn;
+    c.n0 = (int64_t)(j - h * cpn) * YZ_C;
+    c.A = reinterpret_cast<const char*>(g.a + ((bb * g.H + h) * g.T + t0) * g.D);
+    c.E = reinterpret_cast<const char*>(g.b + (int64_t)j * YZ_C * g.D);
+    c.Dc = reinterpret_cast<const char*>(g.dec + (int64_t)j * g.D * YZ_C);
+    c.X = reinterpret_cast<const char*>(g.xy + ((bb * g.H + h) * g.T + t0) * g.N + c.n0);
+    return c;
+  };
+  // x block kb (latents 32 kb ..) of a chunk into the y buffer.
+  auto issue_x = [&](const Bases& c, int kb) {
+    const uint32_t base = lds0 + (uint32_t)(Geo::YBUF + kb * Geo::KB);
+#pragma unroll
+    for (int i = 0; i < Geo::XDMA; ++i)
+      dma16_nt(c.X + kb * 64 + i * stepX, offX, base + (uint32_t)((w + NW * i) * 1024));
+  };
+  // Ring stage of step s of a chunk into slot `slot`: a Y step (s < ny) a_h
+  // rows 0..TM-1 then Ev rows TM..TM+127, a z step the 256 decoder rows.
+  auto issue_stage = [&](const Bases& c, int s, int slot) {
+    const uint32_t base = lds0 + (uint32_t)(slot * Geo::SLOT);
+    if (s < ny) {
+#pragma unroll
+      for (int i = 0; i < TM / 16 / NW; ++i)
+        dma16(c.A + s * 64 + i * stepA, offA, base + (uint32_t)((w + NW * i) * 1024));
+#pragma unroll
+      for (int i = 0; i < 8 / NW; ++i)
+        dma16(c.E + s * 64 + i * (16 * NW * (int64_t)rowA), offA, base + (uint32_t)((TM / 16 + w + NW * i) * 1024));
+    } else {
+#pragma unroll
+      for (int i = 0; i < Geo::ZDMA; ++i)
+        dma16(c.Dc + (s - ny) * 64, offD[i], base + (uint32_t)((w + NW * i) * 1024));
+    }
+  };
+  static_assert(YZ_PREF == 2, "the waits below count one step ahead");
+  // DMAs a wave issues at the top of a step, after its barrier: x blocks 0
+  // and 1 of the next chunk at z step 2 (the z steps before have read those
+  // blocks of y) and blocks 2 and 3 of the current chunk at its first Y step
+  // (the prologue loads chunk jb's four; issued in pairs, the two 64-byte
+  // halves of each 128-byte line are requested together); then the ring
+  // stage of the step YZ_PREF = 2 ahead.  At the top of step (j, s) the wave
+  // has issued after that step's stage (issued at the top of the step 2
+  // back, after that step's x): the x DMAs of step (j, s - 1) and the stage
+  // of the next step; waiting for at most that many leaves the stage (and
+  // every x block issued before it) landed.  At the first z step the
+  // epilogue needs the chunk's blocks 2 and 3 (issued at its first Y step,
+  // at least 2 steps back): there the x count is 0 anyway.
+  auto pending = [&](int j, int s) {
+    int n = 0;
+    if (s == 1 && j > jb) n += 2 * Geo::XDMA;           // x at (j, 0)
+    if (s == ny + 3 && j + 1 < je) n += 2 * Geo::XDMA;  // x at (j, ny + 2)
+    if (s + 1 < per) n += s + 1 < ny ? Geo::YDMA : Geo::ZDMA;  // stage of (j, s + 1)
+    else if (j + 1 < je) n += Geo::YDMA;                // stage of (j + 1, 0)
+    return n;
+  };
+
+  floatx4 accz[4][8];
+  zero_acc(accz);
+  const int yc = w & 1, ym = w >> 1;  // Y^T block: latents 64 yc .., tokens 64 ym ..
+  const int zm = w >> 1, zd = w & 1;  // z block: tokens 64 zm .., columns 128 zd ..
+  const float th = g.relu_th;
+  char* const ybuf = lds + Geo::YBUF;
+  // The two waves of a SIMD issue their DMAs and their MFMAs in opposite
+  // orders, so that one issues MFMAs while the other's DMAs wait in the
+  // texture unit's queue (8 waves: w and w + 4; 4 waves, two workgroups a
+  // CU: the workgroups' barriers are independent).
+  const bool dma_first = NW == 8 ? w < 4 : true;
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no compiler-visible load left in flight
+  Bases cur = bases(jb);
+  if (jb < je) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) issue_x(cur, kb);
+    issue_stage(cur, 0, 0);
+    issue_stage(cur, 1, 1);  // ny >= 2
+  }
+  int slot = 0;  // ring slot of the current step
+  for (int j = jb; j < je; ++j) {
+    const Bases nxt = bases(j + 1 < je ? j + 1 : j);
+    // Stage of the step 2 ahead of (j, s), into the slot the step before
+    // (j, s) used.
+    auto prefetch = [&](int s) {
+      const int t = s + YZ_PREF, sl = slot == 0 ? YZ_RING - 1 : slot - 1;
+      if (t < per) issue_stage(cur, t, sl);
+      else if (j + 1 < je) issue_stage(nxt, t - per, sl);
+    };
+    floatx4 accy[4][4];
+#pragma unroll
+    for (int ci = 0; ci < 4; ++ci)
+#pragma unroll
+      for (int mj = 0; mj < 4; ++mj) accy[ci][mj] = zero4();
+    for (int s = 0; s < ny; ++s) {
+      yz_wait_barrier(pending(j, s));
+      const bf16_t* sp = reinterpret_cast<const bf16_t*>(lds + slot * Geo::SLOT);
+      auto dmas = [&]() {
+        if (s == 0 && j > jb) {
+          issue_x(cur, 2);
+          issue_x(cur, 3);
+        }
+        prefetch(s);
+      };
+      if (dma_first) dmas();
+      mma_64x64_dsasm(sp + TM * BK, sp, lane, 64 * yc, 64 * ym, accy);
+      if (!dma_first) dmas();
+      slot = slot == YZ_RING - 1 ? 0 : slot + 1;
+    }
+    for (int kz = 0; kz < 4; ++kz) {
+      yz_wait_barrier(pending(j, ny + kz));
+      auto dmas = [&]() {
+        if (kz == 2 && j + 1 < je) {
+          issue_x(nxt, 0);
+          issue_x(nxt, 1);
+        }
+        prefetch(ny + kz);
+      };
+      if (dma_first || kz == 0) dmas();
+      if (kz == 0) {
+        // y = act(Y) * x over the x block in place (each lane rewrites only
+        // what it reads; the 4 reads of a latent group are issued before
+        // its writes), then a barrier before any wave reads y.
+#pragma unroll
+        for (int ci = 0; ci < 4; ++ci) {
+          const int cl = 64 * yc + 16 * ci + 4 * (lane >> 4);  // latents cl .. cl + 3 of the chunk
+          float mk[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mk[r] = g.mask ? g.mask[cur.n0 + cl + r] : 1.0f;
+          char* const yb = ybuf + (cl >> 5) * Geo::KB + 8 * ((cl >> 2) & 1);
+          uint2 xv[4];
+#pragma unroll
+          for (int mj = 0; mj < 4; ++mj) {
+            const int ml = 64 * ym + 16 * mj + (lane & 15);
+            xv[mj] = *reinterpret_cast<const uint2*>(yb + 2 * lds_off(ml, (cl >> 3) & 3));
+          }
+#pragma unroll
+          for (int mj = 0; mj < 4; ++mj) {
+            const int ml = 64 * ym + 16 * mj + (lane & 15);
+            const floatx4 v = accy[ci][mj];
+            *reinterpret_cast<uint2*>(yb + 2 * lds_off(ml, (cl >> 3) & 3)) =
+                make_uint2(pack_bf16x2(lowrank_act(v[0], th, mk[0]) * bf16_lo(xv[mj].x),
+                                       lowrank_act(v[1], th, mk[1]) * bf16_hi(xv[mj].x)),
+                           pack_bf16x2(lowrank_act(v[2], th, mk[2]) * bf16_lo(xv[mj].y),
+                                       lowrank_act(v[3], th, mk[3]) * bf16_hi(xv[mj].y)));
+          }
+        }
+        __syncthreads();
+      }
+      const bf16_t* sp = reinterpret_cast<const bf16_t*>(lds + slot * Geo::SLOT);
+      mma_64x128_dsasm(reinterpret_cast<const bf16_t*>(ybuf + kz * Geo::KB), sp, lane, 64 * zm, 128 * zd, accz);
+      if (!dma_first && kz > 0) dmas();
+      slot = slot == YZ_RING - 1 ? 0 : slot + 1;
+    }
+    cur = nxt;
+  }
+  dma_wait_barrier<0>();  // the epilogue reuses the ring
+  epilogue_64x128(accz, reinterpret_cast<bf16_t*>(lds), w, lane, [&](int row, int col, float4 v) {
+    const int64_t m = m0 + 64 * zm + row, d = 128 * zd + col;
+    if (d < g.D) *reinterpret_cast<float4*>(&g.zpart[((int64_t)kp * g.M + m) * g.D + d]) = v;
+  });
+}
+
 // ---- few-row GEMMs (M <= 64 token rows, e.g. one generated token per
 // sequence) ---------------------------------------------------------------
 // The 256 x 128 tile would run 8 (K = 256) or more dependent 32-deep steps on
@@ -286,7 +562,7 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(LayerGemmArgs g) {
   const int kl = 8 * (lane >> 4);  // this lane's 8 k values within a step
   int64_t cb = c0 + (lane & 15);
   cb = cb < ncols ? cb : ncols - 1;
-  const bf16_t* brow = g.b + cb * K + kl;
+  const bf16_t* brow = g.b + (KIND == G_Z ? cb * 128 : cb * K) + kl;
   const bf16_t* arow[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -309,7 +585,7 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(LayerGemmArgs g) {
       const int64_t k = (int64_t)(k0 + s) * 32;
       // Z: k runs over (head, neuron); a 32-deep step stays inside one head.
       const int64_t aoff = KIND == G_Z ? (k / g.N) * g.T * g.N + k % g.N : k;
-      bq[s] = *reinterpret_cast<const bf16x8*>(brow + k);
+      bq[s] = *reinterpret_cast<const bf16x8*>(brow + (KIND == G_Z ? dec_off(0, k, g.D) : k));
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) aq[s][mb] = *reinterpret_cast<const bf16x8*>(arow[mb] + aoff);
     }
@@ -495,10 +771,12 @@ __global__ __launch_bounds__(256) void to_bf16_kernel(const float* __restrict__ 
   }
 }
 
-// out[b, c, r] = bf16(in[b, r, c]) for [batches, rows, cols] (32 x 32 tiles).
+// out[b, c, r] = bf16(in[b, r, c]) for [batches, rows, cols] (32 x 32 tiles);
+// chunked (one batch, rows a multiple of 128): out[dec_off(c, r, cols)], the
+// chunk-major decoder.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const float* __restrict__ in,
                                                              bf16_t* __restrict__ out,
-                                                             int64_t rows, int64_t cols) {
+                                                             int64_t rows, int64_t cols, bool chunked) {
   __shared__ float tile[32][33];
   const int64_t b = blockIdx.z;
   const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
@@ -510,7 +788,7 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const float* __rest
   __syncthreads();
   for (int k = ty; k < 32; k += 8) {
     const int64_t c = c0 + k, r = r0 + tx;
-    if (c < cols && r < rows) out[(b * cols + c) * rows + r] = (bf16_t)tile[tx][k];
+    if (c < cols && r < rows) out[chunked ? dec_off(c, r, cols) : (b * cols + c) * rows + r] = (bf16_t)tile[tx][k];
   }
 }
 
@@ -536,6 +814,29 @@ hipError_t launch_gemm(const LayerGemmArgs& g, hipStream_t st) {
   const int64_t slots = 2 * (int64_t)device_cus();  // two workgroups per CU
   const unsigned grid = (unsigned)(total < slots ? total : slots);
   hipLaunchKernelGGL(layer_gemm_kernel<KIND>, dim3(grid), dim3(NT), 0, st, g);
+  return hipGetLastError();
+}
+
+// Split count of the fused Y + Z launch over the 128-latent chunks, or 0
+// where the shape needs GEMM Y and GEMM Z apart: T a multiple of 256 (a
+// token tile inside one sequence), D a multiple of 64 up to 256 (the z tile),
+// DMA offsets within 32 bits.  About one workgroup per CU, with at least 4
+// chunks each where the chunks allow (C5: 64 token tiles x 4 splits of 64).
+constexpr int YZ_NW = 4;  // waves of the fused launch: 128-token tiles, two workgroups a CU
+constexpr int YZ_TM = YZGeom<YZ_NW>::TM;
+
+int yz_splits(int64_t M, int64_t H, int64_t T, int64_t N, int64_t D) {
+  if (M <= SK_MAXM || T % YZ_TM != 0 || D % 64 != 0 || D > T256) return 0;
+  const int64_t HN = H * N;
+  if (HN % YZ_C != 0 || (int64_t)YZ_TM * N * 2 >= ((int64_t)1 << 32)) return 0;
+  const int64_t tiles = M / YZ_TM, nc = HN / YZ_C;
+  int64_t ks = (int64_t)device_cus() * (8 / YZ_NW) / tiles;
+  if (ks > nc / 4) ks = nc / 4;
+  return (int)(ks < 1 ? 1 : ks);
+}
+
+hipError_t launch_yz(const LayerGemmArgs& g, hipStream_t st) {
+  hipLaunchKernelGGL(layer_yz_kernel<YZ_NW>, dim3((unsigned)(g.mt * g.ks)), dim3(64 * YZ_NW), 0, st, g);
   return hipGetLastError();
 }
 
@@ -607,12 +908,12 @@ bool layer_shape_supported(int64_t N, int64_t D, const char** why) {
 bdh_status pack_lowrank_weights(int64_t H, int64_t N, int64_t D, const float* enc,
                                 const float* encv, const float* dec, bf16_t* enc_p,
                                 bf16_t* encv_p, bf16_t* dec_p, hipStream_t st) {
-  // encoders [H, D, N] -> [H, N, D]; decoder [H*N, D] -> [D, H*N]
+  // encoders [H, D, N] -> [H, N, D]; decoder [H*N, D] -> [H*N/128, D, 128]
   const dim3 ge(cdiv(N, 32), cdiv(D, 32), (unsigned)H);
-  hipLaunchKernelGGL(transpose_bf16_kernel, ge, dim3(256), 0, st, enc, enc_p, D, N);
-  hipLaunchKernelGGL(transpose_bf16_kernel, ge, dim3(256), 0, st, encv, encv_p, D, N);
+  hipLaunchKernelGGL(transpose_bf16_kernel, ge, dim3(256), 0, st, enc, enc_p, D, N, false);
+  hipLaunchKernelGGL(transpose_bf16_kernel, ge, dim3(256), 0, st, encv, encv_p, D, N, false);
   const dim3 gd(cdiv(D, 32), cdiv(H * N, 32), 1);
-  hipLaunchKernelGGL(transpose_bf16_kernel, gd, dim3(256), 0, st, dec, dec_p, H * N, D);
+  hipLaunchKernelGGL(transpose_bf16_kernel, gd, dim3(256), 0, st, dec, dec_p, H * N, D, true);
   BDH_HIP_TRY(hipGetLastError());
   return BDH_OK;
 }
@@ -626,7 +927,7 @@ bdh_status embed_norm(const int32_t* tokens, int64_t n, const float* embed, int6
 bdh_status pack_lm_head(int64_t D, int64_t V, const float* head, bf16_t* packed, hipStream_t st) {
   // [D, V] -> [V, D]
   hipLaunchKernelGGL(transpose_bf16_kernel, dim3(cdiv(V, 32), cdiv(D, 32), 1), dim3(256), 0, st,
-                     head, packed, D, V);
+                     head, packed, D, V, false);
   BDH_HIP_TRY(hipGetLastError());
   return BDH_OK;
 }
@@ -662,8 +963,12 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   // number of 32-deep steps) that give at least two workgroups per CU, at
   // most 16.  Few rows: about 8 steps per wave (32 per workgroup), at most 64.
   const int64_t nkz = HN / 32;
+  // GEMM Y fused into GEMM Z (y never reaches HBM) where the shape allows.
+  const int ks_yz = decode ? 0 : yz_splits(M, a.H, a.T, a.N, a.D);
   int ks = 1;
-  if (M <= SK_MAXM) {
+  if (ks_yz > 0) {
+    ks = ks_yz;
+  } else if (M <= SK_MAXM) {
     while (ks < 64 && nkz / (2 * ks) >= 32) ks *= 2;
   } else {
     const int64_t tiles_z = (int64_t)cdiv(M, T256) * cdiv(a.D, T256 / 2);
@@ -765,15 +1070,23 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   BDH_HIP_TRY(dispatch_per<LnF>((int)a.D, (const float*)attn, (bf16_t*)an, S * a.T, (int)a.D, st));
   g.a = (const bf16_t*)an;
   g.b = a.encv;
-  BDH_HIP_TRY(launch_gemm<G_Y>(g, st));
-  g.a = (const bf16_t*)xy;
-  g.b = a.dec;
-  g.ct = (int)cdiv(a.D, T256 / 2);
-  g.ks = ks;
-  g.zpart = (float*)zp;
-  BDH_HIP_TRY(launch_gemm<G_Z>(g, st));
+  if (ks_yz > 0) {
+    g.dec = a.dec;
+    g.mt = (int)(M / YZ_TM);
+    g.ks = ks;
+    g.zpart = (float*)zp;
+    BDH_HIP_TRY(launch_yz(g, st));
+  } else {
+    BDH_HIP_TRY(launch_gemm<G_Y>(g, st));
+    g.a = (const bf16_t*)xy;
+    g.b = a.dec;
+    g.ct = (int)cdiv(a.D, T256 / 2);
+    g.ks = ks;
+    g.zpart = (float*)zp;
+    BDH_HIP_TRY(launch_gemm<G_Z>(g, st));
+  }
   BDH_HIP_TRY(dispatch_per<ResF>((int)a.D, (const float*)zp, a.cur, a.next, M, (int)a.D, ks, st));
-  if (launches) *launches += 6 + n_attn;
+  if (launches) *launches += (ks_yz > 0 ? 5 : 6) + n_attn;
   return BDH_OK;
 }
 

@@ -27,7 +27,7 @@ from .recurrent import DEFAULT_ROPE_THETA, _ptr, _stream_ptr, supports_backend
 class LowRankWeights(NamedTuple):
     encoder: torch.Tensor      # packed [H, N, D] bf16
     encoder_v: torch.Tensor    # packed [H, N, D] bf16
-    decoder: torch.Tensor      # packed [D, H*N] bf16
+    decoder: torch.Tensor      # packed chunk-major [H*N/128, D, 128] bf16
     heads: int
     latent: int
     embd: int
@@ -51,7 +51,9 @@ class LowRankWeights(NamedTuple):
         dev = enc.device
         ep = torch.empty((H, N, D), device=dev, dtype=torch.bfloat16)
         evp = torch.empty((H, N, D), device=dev, dtype=torch.bfloat16)
-        dp = torch.empty((D, H * N), device=dev, dtype=torch.bfloat16)
+        if (H * N) % 128:
+            return None
+        dp = torch.empty((H * N // 128, D, 128), device=dev, dtype=torch.bfloat16)
         # contiguous copies stay referenced until the launch is enqueued
         enc_c, encv_c, dec_c = enc.contiguous(), encv.contiguous(), decoder.contiguous()
         st = _lib.load().bdh_lowrank_pack_weights(

@@ -237,9 +237,12 @@ typedef struct {
 
 /* The layer's weights in the operand layouts of bdh_lowrank_layer_fwd:
  * encoder, encoder_v [H,D,N] f32 (Burn [1,H,D,N]) -> [H,N,D] bf16;
- * decoder [H*N, D] f32 -> [D, H*N] bf16.  Outputs are caller-owned device
- * buffers of H*N*D bf16 elements each.  Pack once per weight set (the
- * reference shares the weights across layers, dragon.rs:3358). */
+ * decoder [H*N, D] f32 -> chunk-major [H*N/128, D, 128] bf16 (its
+ * transpose in blocks of 128 latents, so that the decoder product reads
+ * one contiguous block per chunk).  Outputs are caller-owned device
+ * buffers of H*N*D bf16 elements each; H*N must be a multiple of 128.
+ * Pack once per weight set (the reference shares the weights across
+ * layers, dragon.rs:3358). */
 bdh_status bdh_lowrank_pack_weights(int64_t heads, int64_t latent, int64_t embd,
                                     const float* encoder, const float* encoder_v,
                                     const float* decoder, void* encoder_packed,

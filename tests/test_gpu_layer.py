@@ -27,6 +27,10 @@ def _case(rng, B, H, T, N, D):
     (1, 1, 40, 256, 2048, 3, True),     # widest embd: 32 values a lane in the LayerNorms
     (2, 1, 160, 256, 1024, 0, False),   # wide embd on the 256 x 128 tiles (M = 320)
     (1, 2, 1000, 512, 64, 3, False),    # context only over 4 gram row blocks, the last ragged
+    # T % 256 == 0 and D <= 256: GEMM Y fused into the decoder (y never stored)
+    (2, 2, 256, 256, 64, 5, False),     # 4 latent chunks over 2 heads in one workgroup per token tile
+    (1, 3, 512, 256, 192, 3, True),     # D = 192 (decoder rows past D clamped), 6 chunks over 3 heads
+    (1, 4, 512, 512, 256, 0, True),     # D = 256, 16 chunks in 4 splits
 ])
 def test_layer_matches_oracle(oracle, B, H, T, N, D, pos, want_rho):
     torch = need_gpu()
@@ -67,7 +71,7 @@ def test_layer_without_rope(oracle):
     assert rel_l2(host(out.next), nref) <= TOL_BF16
 
 
-def test_layer_pack_is_a_transpose(oracle):
+def test_layer_pack_layouts(oracle):
     torch = need_gpu()
     import burn_dragon_amd as bd
     rng = np.random.default_rng(2)
@@ -80,7 +84,9 @@ def test_layer_pack_is_a_transpose(oracle):
     torch.cuda.synchronize()
     assert np.array_equal(host(w.encoder), oracle.round_bf16(enc.transpose(0, 2, 1)))
     assert np.array_equal(host(w.encoder_v), oracle.round_bf16(encv.transpose(0, 2, 1)))
-    assert np.array_equal(host(w.decoder), oracle.round_bf16(dec.T))
+    # decoder: the transpose [D, H N] in 128-latent chunks, [H N / 128, D, 128]
+    chunks = oracle.round_bf16(dec.T).reshape(D, H * N // 128, 128).transpose(1, 0, 2)
+    assert np.array_equal(host(w.decoder), chunks)
 
 
 def test_layer_unsupported_shapes_return_none():
@@ -97,12 +103,13 @@ def test_layer_unsupported_shapes_return_none():
     assert bd.lowrank_layer_forward(dev(torch, cur2), w) is None
 
 
-def test_model_forward_matches_oracle(oracle):
+@pytest.mark.parametrize("T", [130, 256])  # 256: GEMM Y fused into the decoder
+def test_model_forward_matches_oracle(oracle, T):
     # embed -> LN -> 2 shared layers -> logits (vocab 256), every step on the GPU.
     torch = need_gpu()
     import burn_dragon_amd as bd
     rng = np.random.default_rng(77)
-    B, T, V, D, H, N, L = 2, 130, 256, 64, 2, 256, 2
+    B, V, D, H, N, L = 2, 256, 64, 2, 256, 2
     _, enc, encv, dec = _case(rng, 1, H, 1, N, D)
     embed = (rng.standard_normal((V, D)) * 0.02).astype(np.float32)
     head = (rng.standard_normal((D, V)) * 0.02).astype(np.float32)
@@ -223,6 +230,7 @@ def test_model_prompt_then_decode_matches_oracle(oracle):
     (2, 2, 24, 256, 64, 5, "copy", "values"),       # few-row GEMMs, a mask of other values
     (3, 2, 1, 512, 128, 9, "inplace", "blocks"),    # one token in place: the sparse decode step
     (1, 2, 640, 256, 256, 0, "copy", None),         # the threshold alone, two state intervals
+    (1, 2, 512, 256, 128, 6, "copy", "values"),     # fused Y and decoder: mask and threshold in its epilogue
 ])
 def test_layer_threshold_and_mask_match_oracle(oracle, B, H, T, N, D, pos, mode, mask_kind):
     # relu_threshold and the sparse latent mask in both projections
