@@ -407,7 +407,9 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   // of partials).  Measured at C4: chunk 1024 (a tie) 0.83 ms with 1 split,
   // 0.88 with 2; chunk 512 0.875 with 2, 0.889 with 1; 4 splits (the fewest
   // rounds at 512 and 1024) made the context kernel read twice as much
-  // (chunk 512: 157 against 58 us) and the call 0.93-0.98 ms.
+  // (chunk 512: 157 against 58 us) and the call 0.93-0.98 ms; 3 splits at
+  // chunk 512 (4 rounds of 86 steps against 3 of 128) took the gram/readout
+  // and carry launches 0.614 -> 0.602 ms but the call 0.745 -> 0.777 ms.
   const int ndb256 = (int)cdiv(a.D, T256);
   const int rd_pg = nb * ndb256;
   const int64_t slots = device_cus();
