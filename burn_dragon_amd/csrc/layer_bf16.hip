@@ -316,7 +316,9 @@ __device__ __forceinline__ void yz_wait_barrier(int n) {
   }
 }
 
-template <int NW>
+// PLAIN: no threshold and no mask (act = ReLU; the same bits as the general
+// form with th = 0, m = 1, two VALU instructions a value fewer).
+template <int NW, bool PLAIN>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void layer_yz_kernel(LayerGemmArgs g) {
   using Geo = YZGeom<NW>;
   constexpr int TM = Geo::TM;
@@ -433,7 +435,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void layer_yz_kernel(LayerGemmArgs
   // The two waves of a SIMD issue their DMAs and their MFMAs in opposite
   // orders, so that one issues MFMAs while the other's DMAs wait in the
   // texture unit's queue (8 waves: w and w + 4; 4 waves, two workgroups a
-  // CU: the workgroups' barriers are independent).
+  // CU: the workgroups' barriers are independent).  Issuing the DMAs
+  // between the MFMA groups instead (4 waves) was slower: 1.48 against 0.77
+  // ms at C5, the stages landing later and 15 VGPRs spilled.
   const bool dma_first = NW == 8 ? w < 4 : true;
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no compiler-visible load left in flight
   Bases cur = bases(jb);
@@ -490,9 +494,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void layer_yz_kernel(LayerGemmArgs
 #pragma unroll
         for (int ci = 0; ci < 4; ++ci) {
           const int cl = 64 * yc + 16 * ci + 4 * (lane >> 4);  // latents cl .. cl + 3 of the chunk
-          float mk[4];
+          float mk[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+          if (!PLAIN) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) mk[r] = g.mask ? g.mask[cur.n0 + cl + r] : 1.0f;
+            for (int r = 0; r < 4; ++r) mk[r] = g.mask ? g.mask[cur.n0 + cl + r] : 1.0f;
+          }
+          auto act = [&](float v, int r) { return PLAIN ? fmaxf(v, 0.0f) : lowrank_act(v, th, mk[r]); };
           char* const yb = ybuf + (cl >> 5) * Geo::KB + 8 * ((cl >> 2) & 1);
           uint2 xv[4];
 #pragma unroll
@@ -505,10 +512,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void layer_yz_kernel(LayerGemmArgs
             const int ml = 64 * ym + 16 * mj + (lane & 15);
             const floatx4 v = accy[ci][mj];
             *reinterpret_cast<uint2*>(yb + 2 * lds_off(ml, (cl >> 3) & 3)) =
-                make_uint2(pack_bf16x2(lowrank_act(v[0], th, mk[0]) * bf16_lo(xv[mj].x),
-                                       lowrank_act(v[1], th, mk[1]) * bf16_hi(xv[mj].x)),
-                           pack_bf16x2(lowrank_act(v[2], th, mk[2]) * bf16_lo(xv[mj].y),
-                                       lowrank_act(v[3], th, mk[3]) * bf16_hi(xv[mj].y)));
+                make_uint2(pack_bf16x2(act(v[0], 0) * bf16_lo(xv[mj].x), act(v[1], 1) * bf16_hi(xv[mj].x)),
+                           pack_bf16x2(act(v[2], 2) * bf16_lo(xv[mj].y), act(v[3], 3) * bf16_hi(xv[mj].y)));
           }
         }
         __syncthreads();
@@ -836,7 +841,9 @@ int yz_splits(int64_t M, int64_t H, int64_t T, int64_t N, int64_t D) {
 }
 
 hipError_t launch_yz(const LayerGemmArgs& g, hipStream_t st) {
-  hipLaunchKernelGGL(layer_yz_kernel<YZ_NW>, dim3((unsigned)(g.mt * g.ks)), dim3(64 * YZ_NW), 0, st, g);
+  const dim3 grid((unsigned)(g.mt * g.ks)), block(64 * YZ_NW);
+  if (g.relu_th == 0.0f && g.mask == nullptr) hipLaunchKernelGGL((layer_yz_kernel<YZ_NW, true>), grid, block, 0, st, g);
+  else hipLaunchKernelGGL((layer_yz_kernel<YZ_NW, false>), grid, block, 0, st, g);
   return hipGetLastError();
 }
 
