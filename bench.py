@@ -28,6 +28,7 @@ import time
 
 METRIC = "prefill & decode tokens/s per BDH layer (D=256,n=32K); % MFMA / HBM roofline"
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3       # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 SEED = 20260729
 
@@ -656,7 +657,8 @@ def bench_f32(torch, args):
         flop = B * H * T * 4 * N * D
         out[name] = {"shape": {"B": B, "nh": H, "T": T, "N": N, "D": D}, "ms_per_call": round(ms, 4),
                      "tokens_per_s": round(B * T / (ms * 1e-3), 1),
-                     "tflops_recurrent_form": round(flop / (ms * 1e-3) / 1e12, 2)}
+                     "tflops_recurrent_form": round(flop / (ms * 1e-3) / 1e12, 2),
+                     "frac_of_f32_peak": round(flop / (ms * 1e-3) / 1e12 / PEAK_F32_TFLOPS, 4)}
         print(f"[f32] {name}: {ms:.3f} ms/call, {B * T / (ms * 1e-3) / 1e6:.3f} M tok/s, "
               f"{flop / (ms * 1e-3) / 1e12:.1f} TFLOP/s (recurrent form)", flush=True)
         del x, v, ctx, rho
@@ -733,14 +735,15 @@ def bench_ceilings(torch):
 
     mfma = {}
     flop = ctypes.c_double()
-    for name, kind in (("v_mfma_f32_16x16x32_bf16", _lib.BDH_CALIB_MFMA_16X16X32_BF16),
-                       ("v_mfma_f32_32x32x16_bf16", _lib.BDH_CALIB_MFMA_32X32X16_BF16)):
+    for name, kind, peak in (("v_mfma_f32_16x16x32_bf16", _lib.BDH_CALIB_MFMA_16X16X32_BF16, PEAK_BF16_TFLOPS),
+                             ("v_mfma_f32_32x32x16_bf16", _lib.BDH_CALIB_MFMA_32X32X16_BF16, PEAK_BF16_TFLOPS),
+                             ("v_mfma_f32_32x32x2_f32", _lib.BDH_CALIB_MFMA_32X32X2_F32, PEAK_F32_TFLOPS)):
         def call():
             if lib.bdh_calib_mfma(kind, 20000, p(sink), ctypes.byref(flop), stream) != 0:
                 raise RuntimeError(_lib.last_error())
         sec = timed(call, reps=5)
         mfma[name] = {"us": round(sec * 1e6, 1), "TFLOPs": round(flop.value / sec / 1e12, 1),
-                      "frac_of_peak": round(flop.value / sec / 1e12 / PEAK_BF16_TFLOPS, 4)}
+                      "frac_of_peak": round(flop.value / sec / 1e12 / peak, 4)}
         print(f"[ceilings] mfma {name}: {flop.value / sec / 1e12:.0f} TFLOP/s", flush=True)
 
     blas = {}
@@ -756,7 +759,7 @@ def bench_ceilings(torch):
         print(f"[ceilings] hipblaslt {name}: {sec * 1e6:.1f} us, {fl / sec / 1e12:.0f} TFLOP/s", flush=True)
     del q, qt, v
     return {"hbm": hbm, "mfma": mfma, "hipblaslt": blas,
-            "peaks": {"hbm_GBs": PEAK_HBM_GBS, "bf16_TFLOPs": PEAK_BF16_TFLOPS}}
+            "peaks": {"hbm_GBs": PEAK_HBM_GBS, "bf16_TFLOPs": PEAK_BF16_TFLOPS, "f32_TFLOPs": PEAK_F32_TFLOPS}}
 
 
 # --------------------------------------------------------------------------- #

@@ -23,7 +23,7 @@ BDH_BF16 = 1
 
 BDH_KERNEL_PREFILL, BDH_KERNEL_DECODE = 0, 1
 BDH_CALIB_READ, BDH_CALIB_COPY, BDH_CALIB_RMW, BDH_CALIB_RMW_ROWS = 0, 1, 2, 3
-BDH_CALIB_MFMA_16X16X32_BF16, BDH_CALIB_MFMA_32X32X16_BF16 = 0, 1
+BDH_CALIB_MFMA_16X16X32_BF16, BDH_CALIB_MFMA_32X32X16_BF16, BDH_CALIB_MFMA_32X32X2_F32 = 0, 1, 2
 BDH_ROPE_SEQUENTIAL = 0
 BDH_ROPE_FIXED = 1
 

@@ -173,6 +173,25 @@ __global__ __launch_bounds__(kCalibBlock, 2) void calib_mfma_kernel(float* __res
   if (tot == -1.5e38f) sink[0] = tot;  // never true; keeps the chains live
 }
 
+// The fp32 matrix rate (v_mfma_f32_32x32x2f32, the fp32 path's GEMMs): 4
+// independent accumulator chains per wave.
+__global__ __launch_bounds__(kCalibBlock, 2) void calib_mfma_f32_kernel(float* __restrict__ sink, int64_t iters) {
+  const int lane = threadIdx.x & 63;
+  const float a = 0.001f * (float)(lane & 7), b = 0.002f * (float)((lane * 3) & 7);
+  floatx16 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+  for (int64_t i = 0; i < iters; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[j], 0, 0, 0);
+  float tot = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) tot += acc[j][0] + acc[j][15];
+  if (tot == -1.5e38f) sink[0] = tot;  // never true; keeps the chains live
+}
+
 }  // namespace
 }  // namespace bdh
 
@@ -224,6 +243,10 @@ extern "C" bdh_status bdh_calib_mfma(int32_t kind, int64_t iters, float* sink, d
     case BDH_CALIB_MFMA_32X32X16_BF16:
       hipLaunchKernelGGL(calib_mfma_kernel<false>, grid, block, 0, (hipStream_t)stream, sink, iters);
       *flop_out = waves * (double)iters * 4.0 * (2.0 * 32 * 32 * 16);
+      break;
+    case BDH_CALIB_MFMA_32X32X2_F32:
+      hipLaunchKernelGGL(calib_mfma_f32_kernel, grid, block, 0, (hipStream_t)stream, sink, iters);
+      *flop_out = waves * (double)iters * 4.0 * (2.0 * 32 * 32 * 2);
       break;
     default:
       return fail(BDH_EINVAL, "unknown MFMA calibration kind");

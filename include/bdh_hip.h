@@ -408,14 +408,16 @@ bdh_status bdh_calib_hbm(int32_t kind, void* buf, void* buf2, int64_t bytes, con
                          int64_t n_rows, void* stream);
 
 /* MFMA calibration hook, no counterpart in the reference: one launch of
- * `iters` rounds of one bf16 MFMA shape on register operands (8 independent
- * accumulator chains per wave, two waves per SIMD on every CU), the matrix
- * core rate the prefill kernels are read against.  *flop_out receives the
- * launch's FLOP (2 m n k per MFMA); sink is a 4-byte buffer that is never
- * written for these operands. */
+ * `iters` rounds of one MFMA shape on register operands (independent
+ * accumulator chains per wave: 8 for 16x16x32, 4 for the 32x32 shapes; two
+ * waves per SIMD on every CU), the matrix core rate the prefill kernels
+ * (bf16 shapes) and the fp32 path's GEMMs (32x32x2 f32) are read against.
+ * *flop_out receives the launch's FLOP (2 m n k per MFMA); sink is a 4-byte
+ * buffer that is never written for these operands. */
 typedef enum {
   BDH_CALIB_MFMA_16X16X32_BF16 = 0,
-  BDH_CALIB_MFMA_32X32X16_BF16 = 1
+  BDH_CALIB_MFMA_32X32X16_BF16 = 1,
+  BDH_CALIB_MFMA_32X32X2_F32 = 2
 } bdh_calib_mfma_kind;
 bdh_status bdh_calib_mfma(int32_t kind, int64_t iters, float* sink, double* flop_out, void* stream);
 

@@ -23,6 +23,7 @@ pub const BDH_CALIB_RMW: i32 = 2;
 pub const BDH_CALIB_RMW_ROWS: i32 = 3;
 pub const BDH_CALIB_MFMA_16X16X32_BF16: i32 = 0;
 pub const BDH_CALIB_MFMA_32X32X16_BF16: i32 = 1;
+pub const BDH_CALIB_MFMA_32X32X2_F32: i32 = 2;
 
 #[repr(C)]
 #[derive(Clone, Copy, Debug, Default)]

@@ -58,7 +58,8 @@ def test_mfma_calibration_reports_its_flop():
     announce("calib mfma")
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     for kind, per_mfma, per_round in ((_lib.BDH_CALIB_MFMA_16X16X32_BF16, 2 * 16 * 16 * 32, 8),
-                                      (_lib.BDH_CALIB_MFMA_32X32X16_BF16, 2 * 32 * 32 * 16, 4)):
+                                      (_lib.BDH_CALIB_MFMA_32X32X16_BF16, 2 * 32 * 32 * 16, 4),
+                                      (_lib.BDH_CALIB_MFMA_32X32X2_F32, 2 * 32 * 32 * 2, 4)):
         assert lib.bdh_calib_mfma(kind, 100, ctypes.c_void_p(sink.data_ptr()), ctypes.byref(flop),
                                   stream) == _lib.BDH_OK
         torch.cuda.synchronize()
