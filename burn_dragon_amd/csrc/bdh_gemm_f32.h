@@ -265,7 +265,10 @@ inline bool vec_ok(const float* X, int64_t so, int64_t si, int64_t sr, int64_t s
 // fp32 C2 shape, was slower: 5 ranges 523 us, 16 ranges 384 us, against 351
 // us with 4: the masked tiles' workgroups, which exit at once, still take
 // dispatch slots.  Aiming at four workgroups per CU, which registers and LDS
-// allow, gave the gram and readout 8 ranges and no gain: 362 and 332 us.)
+// allow, gave the gram and readout 8 ranges and no gain: 362 and 332 us; a
+// grid of the gram's working tiles only, 8 ranges, 3 workgroups on every
+// CU: 352 us.  Counters put the GEMMs' MFMAs 46-66 % busy whatever the
+// occupancy.)
 inline int split_k_ranges(int64_t tiles, int K) {
   int p = 1;
   const int64_t want = 2 * (int64_t)device_cus();
