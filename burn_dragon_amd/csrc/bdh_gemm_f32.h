@@ -17,7 +17,10 @@
 // epilogue.
 #pragma once
 
+#include <type_traits>
+
 #include "bdh_internal.h"
+#include "bdh_mfma.h"
 
 namespace bdh {
 namespace gf32 {
@@ -48,6 +51,7 @@ struct GemmF32 {
   float* part;          // split-K partials [ksplit, batch, M, N] (ksplit > 1)
   int ksplit;
   int64_t batch;
+  int tri;              // direct-load grid of the tiles on or below the diagonal only (M == N, split-K)
 };
 
 constexpr int GT = 128;   // tile edge
@@ -120,18 +124,34 @@ __device__ __forceinline__ int frag_k(int64_t sr, int64_t sk, int t, int e) {
   return (sr == 1 && sk != 1) ? t / TPK : (t & 1) * FE + e;
 }
 
+// The epilogue's addend: C itself (the accumulating kinds), src (E_CARRY),
+// or none.
 template <int EPI>
-__device__ __forceinline__ void epilogue(const GemmF32& g, int64_t bo, int64_t bi, float d, float carry, int m,
-                                         int n, float v) {
-  float* C = g.C + bo * g.sCo + bi * g.sCi;
+__device__ __forceinline__ const float* epi_addend(const GemmF32& g, int64_t bo, int64_t bi) {
+  if (EPI == E_ROWSCALE_ACC || EPI == E_ROWREV_ACC) return g.C + bo * g.sCo + bi * g.sCi;
+  if (EPI == E_CARRY && g.src) return g.src + bo * g.sCo + bi * g.sCi;
+  return nullptr;
+}
+
+// Output value of (m, n) from the sum v and the addend x (when the kind has one).
+template <int EPI>
+__device__ __forceinline__ float epi_value(const GemmF32& g, float d, float carry, int m, int n, float v, float x) {
   if (EPI == E_TRIL) v = n < m ? v : 0.0f;
   if (EPI == E_TRIL_DECAY) v = n < m ? (g.decay ? v * dpowf(d, m - n) : v) : 0.0f;
   if ((EPI == E_ROWSCALE || EPI == E_ROWSCALE_ACC) && g.decay) v *= dpowf(d, m);
   if (EPI == E_ROWREV_ACC && g.decay) v *= dpowf(d, g.kpow - m);
+  if (EPI == E_ROWSCALE_ACC || EPI == E_ROWREV_ACC) v += x;
+  if (EPI == E_CARRY && g.src) v += x * carry;
+  return v;
+}
+
+template <int EPI>
+__device__ __forceinline__ void epilogue(const GemmF32& g, int64_t bo, int64_t bi, float d, float carry, int m,
+                                         int n, float v) {
+  float* C = g.C + bo * g.sCo + bi * g.sCi;
+  const float* X = epi_addend<EPI>(g, bo, bi);
   const int64_t o = (int64_t)m * g.sCm + (int64_t)n * g.sCn;
-  if (EPI == E_ROWSCALE_ACC || EPI == E_ROWREV_ACC) v += C[o];
-  if (EPI == E_CARRY && g.src) v += g.src[bo * g.sCo + bi * g.sCi + o] * carry;
-  C[o] = v;
+  C[o] = epi_value<EPI>(g, d, carry, m, n, v, X ? X[o] : 0.0f);
 }
 
 template <int EPI, bool KSCALE>
@@ -250,6 +270,269 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmF32 g) {
   epilogue<EPI>(g, bo, bi, d, carry, m, n, v);
 }
 
+// --- Direct-load kernel: the shapes the fp32 forward and backward run ----
+// The product and epilogues of gemm_f32_kernel, with the operand tiles
+// fetched by direct global -> LDS loads (global_load_lds_dwordx4) into a
+// ring of DST stages, DST - 1 of them in flight while one is multiplied:
+// the register-staged kernel above has one step in flight, and its MFMAs
+// sat 46-66 % busy.  Each operand is either
+//   KC, contiguous along k (sk == 1): tile [128 rows][16 k] of 64-byte
+//       rows, 16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 3);
+//   RC, contiguous along its rows (sr == 1): tile [16 k][128 rows] of
+//       512-byte rows, chunk c of k row k stored at chunk c ^ 4 ((k >> 2) & 3).
+// The swizzles keep the fragment reads free of bank conflicts; a DMA writes
+// lane l's 16 bytes to LDS at M0 + 16 l, so it applies them by the choice of
+// the global chunk each lane fetches.  Rows past the operand's end re-read
+// its last row (KC) or chunk (RC): their sums are never written.
+// MFMA: v_mfma_f32_16x16x4f32, lane l = 16 g + i holding row (column) i of a
+// 16 x 16 block in k slot g.  The 4 MFMAs j = 0..3 of a 16-deep step give
+// slot g the k index 4 g + j for both operands, so a KC operand reads its 4
+// values in one 16-byte read and an RC operand in two 2-dword reads (k rows
+// 4 g + j, 512 bytes apart).  A wave owns a 64 x 64 block: 4 x 4 MFMA
+// blocks, 64 MFMAs a step.
+// Workgroup ids are remapped so that each XCD (id % 8) takes a contiguous
+// range of tiles: the tiles of one batch and K range, which share operand
+// rows, then run on one L2.
+constexpr int DST = 4;               // ring stages
+constexpr int DTILE = GT * GK * 4;   // bytes of one operand tile (8 KiB)
+constexpr int DSTAGE = 2 * DTILE;    // A tile, then B tile
+constexpr int DSCALE = 1024;         // KSCALE: most k of one workgroup (LDS table of d^(kpow - k))
+
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+// Byte offset from a tile's global base of what lane `lane` of DMA
+// instruction i (8 per tile) fetches; R = rows of the tile inside the operand.
+__device__ __forceinline__ uint32_t dma_src(bool kc, int64_t sr, int64_t sk, int R, int i, int lane) {
+  if (kc) {
+    const int r = 16 * i + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 1) & 3);
+    return (uint32_t)((int64_t)min(r, R - 1) * sr * 4 + c * 16);
+  }
+  const int k = 2 * i + (lane >> 5);
+  const int c = min((lane & 31) ^ (4 * ((k >> 2) & 3)), R / 4 - 1);
+  return (uint32_t)((int64_t)k * sk * 4 + c * 16);
+}
+
+// KC fragments: v[mi] = k slots 4 g .. 4 g + 3 of row 16 mi + i of the wave's
+// block (a = the lane's address of mi = 0).
+__device__ __forceinline__ void dread_kc(uint32_t a, floatx4 (&v)[4]) {
+  asm volatile("ds_read_b128 %0, %1 offset:0" : "=v"(v[0]) : "v"(a));
+  asm volatile("ds_read_b128 %0, %1 offset:1024" : "=v"(v[1]) : "v"(a));
+  asm volatile("ds_read_b128 %0, %1 offset:2048" : "=v"(v[2]) : "v"(a));
+  asm volatile("ds_read_b128 %0, %1 offset:3072" : "=v"(v[3]) : "v"(a));
+}
+// RC fragments: v[mi][h] = k rows 4 g + 2 h and 4 g + 2 h + 1 of column
+// 16 mi + i (a[mi] = the lane's address of k row 4 g).
+__device__ __forceinline__ void dread_rc(const uint32_t (&a)[4], floatx2 (&v)[4][2]) {
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    asm volatile("ds_read2st64_b32 %0, %1 offset0:0 offset1:2" : "=v"(v[mi][0]) : "v"(a[mi]));
+    asm volatile("ds_read2st64_b32 %0, %1 offset0:4 offset1:6" : "=v"(v[mi][1]) : "v"(a[mi]));
+  }
+}
+__device__ __forceinline__ void dtie(floatx4 (&v)[4]) {
+  asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+}
+__device__ __forceinline__ void dtie(floatx2 (&v)[4][2]) {
+  asm volatile("" : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[1][0]), "+v"(v[1][1]), "+v"(v[2][0]), "+v"(v[2][1]),
+               "+v"(v[3][0]), "+v"(v[3][1]));
+}
+__device__ __forceinline__ float dval(const floatx4 (&v)[4], int mi, int j) { return v[mi][j]; }
+__device__ __forceinline__ float dval(const floatx2 (&v)[4][2], int mi, int j) { return v[mi][j >> 1][j & 1]; }
+
+template <bool KC>
+using DFrag = typename std::conditional<KC, floatx4[4], floatx2[4][2]>::type;
+
+template <int EPI, bool KSCALE, bool AKC, bool BKC>
+__global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmF32 g, int ntx, int nty) {
+  __shared__ __attribute__((aligned(16))) char lds[DST * DSTAGE + (KSCALE ? 4 * DSCALE : 0)];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int wm = w >> 1, wn = w & 1, gq = lane >> 4, li = lane & 15;
+  // XCD-contiguous work order (the launch has a multiple of 8 workgroups).
+  const int nwg = (int)gridDim.x, id = (int)blockIdx.x;
+  int wk = (nwg & 7) ? id : (id & 7) * (nwg >> 3) + (id >> 3);
+  int tx, ty;
+  int64_t z;
+  if (g.tri) {
+    // Tiles (ty, tx <= ty) in row order, nty (nty + 1) / 2 of them a batch.
+    const int per = nty * (nty + 1) / 2;
+    z = wk / per;
+    int r = wk - (int)z * per;
+    ty = 0;
+    while (r > ty) {
+      r -= ty + 1;
+      ++ty;
+    }
+    tx = r;
+  } else {
+    tx = wk % ntx;
+    wk /= ntx;
+    ty = wk % nty;
+    z = wk / nty;
+  }
+  const int P = g.ksplit > 1 ? g.ksplit : 1;
+  const int kp = (int)(z % P);
+  const int64_t b = z / P, bo = b / g.H, bi = b - bo * g.H;
+  const int m0 = ty * GT, n0 = tx * GT;
+  const float d = g.decay ? g.decay[bi] : 1.0f;
+  const bool tril = EPI == E_TRIL || EPI == E_TRIL_DECAY;
+  if (tril && n0 >= m0 + GT) {
+    if (P > 1) return;
+    float* C = g.C + bo * g.sCo + bi * g.sCi;
+    for (int i = t; i < GT * GT; i += 256) {
+      const int m = m0 + i / GT, n = n0 + i % GT;
+      if (m < g.M && n < g.N) C[(int64_t)m * g.sCm + (int64_t)n * g.sCn] = 0.0f;
+    }
+    return;
+  }
+  const int Kfull = g.kcausal ? min(g.K, m0 + GT) : g.K;
+  const int chunk = ((Kfull + P - 1) / P + GK - 1) / GK * GK;
+  const int k_lo = min(Kfull, kp * chunk);
+  const int Kt = min(Kfull, k_lo + chunk);
+  const int nks = (Kt - k_lo) / GK;  // the host sends K % GK == 0 here
+  const int Ma = min(GT, g.M - m0), Nb = min(GT, g.N - n0);
+  const char* Ag = reinterpret_cast<const char*>(g.A + bo * g.sAo + bi * g.sAi + (int64_t)m0 * g.sAm +
+                                                 (int64_t)k_lo * g.sAk);
+  const char* Bg = reinterpret_cast<const char*>(g.B + bo * g.sBo + bi * g.sBi + (int64_t)n0 * g.sBn +
+                                                 (int64_t)k_lo * g.sBk);
+  const int64_t a_step = (int64_t)GK * g.sAk * 4, b_step = (int64_t)GK * g.sBk * 4;
+  uint32_t va[2], vb[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    va[j] = dma_src(AKC, g.sAm, g.sAk, Ma, w + 4 * j, lane);
+    vb[j] = dma_src(BKC, g.sBn, g.sBk, Nb, w + 4 * j, lane);
+  }
+  const uint32_t l0 = mfma::lds_addr(lds);
+  auto issue = [&](int s) {
+    const uint32_t st = l0 + (uint32_t)((s % DST) * DSTAGE);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) mfma::dma16(Ag + s * a_step, va[j], st + (uint32_t)((w + 4 * j) * 1024));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) mfma::dma16(Bg + s * b_step, vb[j], st + (uint32_t)(DTILE + (w + 4 * j) * 1024));
+  };
+
+  const bool ksc = KSCALE && g.decay != nullptr;
+  float* sct = reinterpret_cast<float*>(lds + DST * DSTAGE);
+  if (ksc) {
+    for (int k = t; k < Kt - k_lo; k += 256) sct[k] = dpowf(d, g.kpow - (k_lo + k));
+    __syncthreads();
+  }
+
+  // Lane addresses of the fragments, relative to a stage.
+  const uint32_t a_kc = (uint32_t)((wm * 64 + li) * 64 + ((gq ^ ((li >> 1) & 3)) << 4));
+  const uint32_t b_kc = (uint32_t)(DTILE + (wn * 64 + li) * 64 + ((gq ^ ((li >> 1) & 3)) << 4));
+  uint32_t a_rc[4], b_rc[4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    a_rc[mi] = (uint32_t)(2048 * gq + 256 * wm + 64 * (mi ^ gq) + 4 * li);
+    b_rc[mi] = (uint32_t)(DTILE + 2048 * gq + 256 * wn + 64 * (mi ^ gq) + 4 * li);
+  }
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
+
+  // A whole tile's epilogue addends are loaded before the K loop, so that
+  // their latency hides behind it (they complete before the first stage's
+  // DMAs, which are issued after them).
+  constexpr bool ADDEND = EPI == E_ROWSCALE_ACC || EPI == E_ROWREV_ACC || EPI == E_CARRY;
+  const bool whole = P == 1 && m0 + GT <= g.M && n0 + GT <= g.N;
+  const float* X = epi_addend<EPI>(g, bo, bi);
+  float xv[ADDEND ? 4 : 1][4][4];
+  if (ADDEND && whole && X) {
+#pragma unroll
+    for (int mi = 0; mi < (ADDEND ? 4 : 1); ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * 64 + 16 * mi + 4 * gq + r, n = n0 + wn * 64 + 16 * ni + li;
+          xv[mi][ni][r] = X[(int64_t)m * g.sCm + (int64_t)n * g.sCn];
+        }
+  }
+
+  for (int s = 0; s < DST - 1 && s < nks; ++s) issue(s);
+  for (int s = 0; s < nks; ++s) {
+    // Stage s has landed once at most the DMAs of the stages issued after
+    // it (4 a stage) are in flight.
+    const int later = min(DST - 2, nks - 1 - s);
+    if (later >= 2) mfma::dma_wait_barrier<8>();
+    else if (later == 1) mfma::dma_wait_barrier<4>();
+    else mfma::dma_wait_barrier<0>();
+    // The slot of stage s - 1, which every wave finished reading before the barrier.
+    if (s + DST - 1 < nks) issue(s + DST - 1);
+    const uint32_t st = l0 + (uint32_t)((s % DST) * DSTAGE);
+    DFrag<AKC> fa;
+    DFrag<BKC> fb;
+    if constexpr (AKC) {
+      dread_kc(st + a_kc, fa);
+    } else {
+      const uint32_t ad[4] = {st + a_rc[0], st + a_rc[1], st + a_rc[2], st + a_rc[3]};
+      dread_rc(ad, fa);
+    }
+    if constexpr (BKC) {
+      dread_kc(st + b_kc, fb);
+    } else {
+      const uint32_t bd[4] = {st + b_rc[0], st + b_rc[1], st + b_rc[2], st + b_rc[3]};
+      dread_rc(bd, fb);
+    }
+    floatx4 sc = floatx4{1.0f, 1.0f, 1.0f, 1.0f};
+    if (KSCALE && ksc) {
+      const uint32_t sa = mfma::lds_addr(sct) + (uint32_t)(64 * s + 16 * gq);
+      asm volatile("ds_read_b128 %0, %1" : "=v"(sc) : "v"(sa));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sc));
+    dtie(fa);
+    dtie(fb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        av[mi] = dval(fa, mi, j);
+        if (KSCALE) av[mi] *= sc[j];
+        bv[mi] = dval(fb, mi, j);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mi], bv[ni], acc[mi][ni], 0, 0, 0);
+    }
+  }
+
+  const float carry = (EPI == E_CARRY && g.decay) ? dpowf(d, g.kpow) : 1.0f;
+  float* Pp = P > 1 ? g.part + ((int64_t)kp * g.batch + b) * (int64_t)g.M * g.N : nullptr;
+  // Block (mi, ni), register r: row 16 mi + 4 g + r, column 16 ni + i.
+  if (whole) {
+    float* C = g.C + bo * g.sCo + bi * g.sCi;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * 64 + 16 * mi + 4 * gq + r, n = n0 + wn * 64 + 16 * ni + li;
+          const float x = (ADDEND && X) ? xv[ADDEND ? mi : 0][ni][r] : 0.0f;
+          C[(int64_t)m * g.sCm + (int64_t)n * g.sCn] = epi_value<EPI>(g, d, carry, m, n, acc[mi][ni][r], x);
+        }
+    return;
+  }
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 64 + 16 * mi + 4 * gq + r, n = n0 + wn * 64 + 16 * ni + li;
+        if (m >= g.M || n >= g.N) continue;
+        if (P > 1) Pp[(int64_t)m * g.N + n] = acc[mi][ni][r];
+        else epilogue<EPI>(g, bo, bi, d, carry, m, n, acc[mi][ni][r]);
+      }
+}
+
 // 16-byte loads need the operand's base, batch strides and the stride of
 // the non-contiguous index to keep 4-float alignment.
 inline bool vec_ok(const float* X, int64_t so, int64_t si, int64_t sr, int64_t sk) {
@@ -257,6 +540,17 @@ inline bool vec_ok(const float* X, int64_t so, int64_t si, int64_t sr, int64_t s
   if (sk == 1) return sr % 4 == 0;
   if (sr == 1) return sk % 4 == 0;
   return false;
+}
+
+// Layout of an operand for the direct-load kernel: 1 = contiguous along k
+// (KC), 0 = contiguous along its rows (RC, R rows a multiple of 4), -1 = not
+// served (no 16-byte alignment, neither index contiguous, or a tile's DMA
+// offsets past 32 bits).
+inline int dma_layout(const float* X, int64_t so, int64_t si, int64_t sr, int64_t sk, int R) {
+  if (!vec_ok(X, so, si, sr, sk)) return -1;
+  if (sk == 1 && (int64_t)(GT - 1) * sr * 4 + 64 <= (int64_t)UINT32_MAX) return 1;
+  if (sr == 1 && R % 4 == 0 && (int64_t)(GK - 1) * sk * 4 + 512 <= (int64_t)UINT32_MAX) return 0;
+  return -1;
 }
 
 // Ranges of K to split into: the fewest (a power of two, up to 16) that give
@@ -276,6 +570,16 @@ inline int split_k_ranges(int64_t tiles, int K) {
   return p;
 }
 
+// Ranges for the direct-load kernel: as many as fit its workgroups of the
+// working tiles into the CUs' two slots (up to 16), each at least 256 deep.
+// (The gram at the fp32 C2 shape: 96 working tiles, 5 ranges, 480 workgroups.)
+inline int split_k_ranges_dma(int64_t work_tiles, int K) {
+  int64_t p = 2 * (int64_t)device_cus() / (work_tiles > 0 ? work_tiles : 1);
+  p = p < 16 ? p : 16;
+  p = p < K / 256 ? p : K / 256;
+  return p > 1 ? (int)p : 1;
+}
+
 // C = epilogue(A B^T) over `batch` products.  With `part` (part_elems floats)
 // a long K may be split; the partials need ksplit * batch * M * N floats.
 template <int EPI, bool KSCALE = false>
@@ -286,12 +590,42 @@ hipError_t gemm(GemmF32 g, int64_t batch, hipStream_t st, float* part = nullptr,
   g.b_vec = vec_ok(g.B, g.sBo, g.sBi, g.sBn, g.sBk);
   g.batch = batch;
   const int64_t tiles = ((g.N + GT - 1) / GT) * ((g.M + GT - 1) / GT) * batch;
-  int p = part ? split_k_ranges(tiles, g.K) : 1;
-  while (p > 1 && (size_t)p * (size_t)batch * (size_t)g.M * (size_t)g.N > part_elems) p /= 2;
+  const int ntx = (g.N + GT - 1) / GT, nty = (g.M + GT - 1) / GT;
+  const int akc = dma_layout(g.A, g.sAo, g.sAi, g.sAm, g.sAk, g.M), bkc = dma_layout(g.B, g.sBo, g.sBi, g.sBn, g.sBk, g.N);
+  const bool dma = akc >= 0 && bkc >= 0 && g.K % GK == 0 && (!KSCALE || g.K <= DSCALE);
+  const bool tril = EPI == E_TRIL || EPI == E_TRIL_DECAY;
+  const int64_t tri_tiles = (int64_t)nty * (nty + 1) / 2 * batch;
+  const size_t per = (size_t)batch * (size_t)g.M * (size_t)g.N;
+  int p = 1;
+  if (part && dma) {
+    p = split_k_ranges_dma(tril && g.M == g.N && !g.kcausal ? tri_tiles : tiles, g.K);
+    if ((size_t)p * per > part_elems) p = (int)(part_elems / per);
+  } else if (part) {
+    p = split_k_ranges(tiles, g.K);
+    while (p > 1 && (size_t)p * per > part_elems) p /= 2;
+  }
+  if (p < 1) p = 1;
   g.ksplit = p;
   g.part = p > 1 ? part : nullptr;
-  const dim3 grid((unsigned)((g.N + GT - 1) / GT), (unsigned)((g.M + GT - 1) / GT), (unsigned)(batch * p));
-  hipLaunchKernelGGL((gemm_f32_kernel<EPI, KSCALE>), grid, dim3(256), 0, st, g);
+  // Masked tiles are left out of the grid only with split-K, whose reduce
+  // writes their zeros.
+  g.tri = dma && tril && g.M == g.N && !g.kcausal && p > 1;
+  if (dma) {
+    const int64_t nwg = (g.tri ? tri_tiles : tiles) * p;
+    if (nwg > INT32_MAX) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)nwg);
+    if (akc && bkc)
+      hipLaunchKernelGGL((gemm_f32_dma_kernel<EPI, KSCALE, true, true>), grid, dim3(256), 0, st, g, ntx, nty);
+    else if (akc)
+      hipLaunchKernelGGL((gemm_f32_dma_kernel<EPI, KSCALE, true, false>), grid, dim3(256), 0, st, g, ntx, nty);
+    else if (bkc)
+      hipLaunchKernelGGL((gemm_f32_dma_kernel<EPI, KSCALE, false, true>), grid, dim3(256), 0, st, g, ntx, nty);
+    else
+      hipLaunchKernelGGL((gemm_f32_dma_kernel<EPI, KSCALE, false, false>), grid, dim3(256), 0, st, g, ntx, nty);
+  } else {
+    const dim3 grid((unsigned)ntx, (unsigned)nty, (unsigned)(batch * p));
+    hipLaunchKernelGGL((gemm_f32_kernel<EPI, KSCALE>), grid, dim3(256), 0, st, g);
+  }
   if (p > 1) {
     const int64_t total = batch * (int64_t)g.M * g.N;
     hipLaunchKernelGGL(gemm_reduce_kernel<EPI>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, g);
@@ -303,7 +637,12 @@ hipError_t gemm(GemmF32 g, int64_t batch, hipStream_t st, float* part = nullptr,
 // Partial floats the split-K of a [batch, M, N] product at depth K may use.
 inline size_t split_k_elems(int64_t batch, int M, int N, int K) {
   const int64_t tiles = ((N + GT - 1) / GT) * (int64_t)((M + GT - 1) / GT) * batch;
-  const int p = split_k_ranges(tiles, K);
+  const int64_t nty = (M + GT - 1) / GT;
+  int p = split_k_ranges(tiles, K);
+  // Either kernel's count; the direct-load one's is largest with the
+  // triangular grid of a square masked product.
+  const int pd = split_k_ranges_dma(M == N ? nty * (nty + 1) / 2 * batch : tiles, K);
+  p = p > pd ? p : pd;
   return p > 1 ? (size_t)p * (size_t)batch * (size_t)M * (size_t)N : 0;
 }
 
