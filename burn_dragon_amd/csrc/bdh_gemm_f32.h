@@ -434,35 +434,28 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmF32 g, int ntx
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
 
-  // A whole tile's epilogue addends are loaded before the K loop, so that
-  // their latency hides behind it (they complete before the first stage's
-  // DMAs, which are issued after them).
+  // A whole tile's epilogue addends are loaded during the last K steps (the
+  // rows of block rows 0-1 in step nks - 3, of 2-3 in step nks - 2, once no
+  // DMA is left to issue), so that their latency hides behind those steps.
   constexpr bool ADDEND = EPI == E_ROWSCALE_ACC || EPI == E_ROWREV_ACC || EPI == E_CARRY;
   const bool whole = P == 1 && m0 + GT <= g.M && n0 + GT <= g.N;
   const float* X = epi_addend<EPI>(g, bo, bi);
   float xv[ADDEND ? 4 : 1][4][4];
-  if (ADDEND && whole && X) {
+  auto load_addends = [&](int mi0) {
 #pragma unroll
-    for (int mi = 0; mi < (ADDEND ? 4 : 1); ++mi)
+    for (int mi = mi0; mi < mi0 + 2; ++mi)
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m0 + wm * 64 + 16 * mi + 4 * gq + r, n = n0 + wn * 64 + 16 * ni + li;
-          xv[mi][ni][r] = X[(int64_t)m * g.sCm + (int64_t)n * g.sCn];
+          xv[ADDEND ? mi : 0][ni][r] = X[(int64_t)m * g.sCm + (int64_t)n * g.sCn];
         }
-  }
+  };
+  const bool early = ADDEND && whole && X != nullptr && nks >= DST - 1;
 
-  for (int s = 0; s < DST - 1 && s < nks; ++s) issue(s);
-  for (int s = 0; s < nks; ++s) {
-    // Stage s has landed once at most the DMAs of the stages issued after
-    // it (4 a stage) are in flight.
-    const int later = min(DST - 2, nks - 1 - s);
-    if (later >= 2) mfma::dma_wait_barrier<8>();
-    else if (later == 1) mfma::dma_wait_barrier<4>();
-    else mfma::dma_wait_barrier<0>();
-    // The slot of stage s - 1, which every wave finished reading before the barrier.
-    if (s + DST - 1 < nks) issue(s + DST - 1);
+  // Reads and MFMAs of stage s (after the wait that it has landed).
+  auto step = [&](int s) {
     const uint32_t st = l0 + (uint32_t)((s % DST) * DSTAGE);
     DFrag<AKC> fa;
     DFrag<BKC> fb;
@@ -501,6 +494,39 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmF32 g, int ntx
         for (int ni = 0; ni < 4; ++ni)
           acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mi], bv[ni], acc[mi][ni], 0, 0, 0);
     }
+  };
+
+  // Stage s has landed once at most the vector memory operations issued
+  // after it are in flight: the DMAs of later stages (4 a stage) and, in the
+  // last two steps of the early-addend tail, the addend loads (32 a step; 63
+  // is the counter's most, one load short).
+  for (int s = 0; s < DST - 1 && s < nks; ++s) issue(s);
+  int s = 0;
+  for (; s + DST - 1 < nks; ++s) {
+    mfma::dma_wait_barrier<4 * (DST - 2)>();
+    // Into the slot of stage s - 1, which every wave finished reading before the barrier.
+    issue(s + DST - 1);
+    step(s);
+  }
+  static_assert(DST == 4, "the tails below wait for 2, 1, 0 later stages");
+  if (early) {
+    // nks >= 3: the last three stages, none left to issue.
+    mfma::dma_wait_barrier<8>();
+    load_addends(0);
+    step(s);
+    mfma::dma_wait_barrier<36>();
+    load_addends(2);
+    step(s + 1);
+    mfma::dma_wait_barrier<63>();
+    step(s + 2);
+  } else {
+    for (; s < nks; ++s) {
+      const int later = nks - 1 - s;
+      if (later >= 2) mfma::dma_wait_barrier<8>();
+      else if (later == 1) mfma::dma_wait_barrier<4>();
+      else mfma::dma_wait_barrier<0>();
+      step(s);
+    }
   }
 
   const float carry = (EPI == E_CARRY && g.decay) ? dpowf(d, g.kpow) : 1.0f;
@@ -508,6 +534,10 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmF32 g, int ntx
   // Block (mi, ni), register r: row 16 mi + 4 g + r, column 16 ni + i.
   if (whole) {
     float* C = g.C + bo * g.sCo + bi * g.sCi;
+    if (ADDEND && X != nullptr && !early) {
+      load_addends(0);
+      load_addends(2);
+    }
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -571,12 +601,16 @@ inline int split_k_ranges(int64_t tiles, int K) {
 }
 
 // Ranges for the direct-load kernel: as many as fit its workgroups of the
-// working tiles into the CUs' two slots (up to 16), each at least 256 deep.
-// (The gram at the fp32 C2 shape: 96 working tiles, 5 ranges, 480 workgroups.)
+// working tiles into the CUs' two slots (up to 16), each at least 128 deep;
+// a short K (< 1024) only when the tiles fill under a quarter of the CUs.
+// (At the fp32 C2 shape: the gram's 96 working tiles 5 ranges, 480
+// workgroups; the readout 4; S V, K = 256 on 128 tiles, none: 2 ranges took
+// 19.9 us and their reduce 10.6 us, against 22.7 us unsplit.)
 inline int split_k_ranges_dma(int64_t work_tiles, int K) {
+  if (K < 1024 && work_tiles * 4 >= (int64_t)device_cus()) return 1;
   int64_t p = 2 * (int64_t)device_cus() / (work_tiles > 0 ? work_tiles : 1);
   p = p < 16 ? p : 16;
-  p = p < K / 256 ? p : K / 256;
+  p = p < K / 128 ? p : K / 128;
   return p > 1 ? (int)p : 1;
 }
 

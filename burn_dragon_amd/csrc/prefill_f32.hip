@@ -19,12 +19,14 @@ namespace bdh {
 
 using namespace gf32;
 
-// Split-K partials of the two long products (gram and readout, K = N).
+// Split-K partials of the gram and readout (K = N) and of S V (K = L).
 size_t f32_path_part_elems(const F32Args& a) {
   const int64_t S = a.B * a.H;
   const int L = (int)(a.T < a.Lmax ? a.T : a.Lmax);
   const size_t g = split_k_elems(S, L, L, (int)a.N), r = split_k_elems(S, L, (int)a.D, (int)a.N);
-  return g > r ? g : r;
+  const size_t sv = split_k_elems(S, L, (int)a.D, L);
+  const size_t m = g > r ? g : r;
+  return m > sv ? m : sv;
 }
 
 hipError_t run_f32_path(const F32Args& a, hipStream_t st, uint64_t* launches) {
@@ -54,7 +56,7 @@ hipError_t run_f32_path(const F32Args& a, hipStream_t st, uint64_t* launches) {
     g.C = a.ctx + t0 * D; g.sCo = H * T * D; g.sCi = T * D; g.sCm = D; g.sCn = 1;
     g.M = (int)L; g.N = (int)D; g.K = (int)L;
     g.kcausal = 1;
-    e = gemm<E_STORE>(g, S, st, nullptr, 0, &n);
+    e = gemm<E_STORE>(g, S, st, a.part, pe, &n);
     if (e != hipSuccess) return e;
     if (rho_cur) {
       // ctx += (Q * d^r) rho
