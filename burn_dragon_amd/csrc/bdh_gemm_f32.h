@@ -293,6 +293,9 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmF32 g) {
 // Workgroup ids are remapped so that each XCD (id % 8) takes a contiguous
 // range of tiles: the tiles of one batch and K range, which share operand
 // rows, then run on one L2.
+// (Reading a step's fragments while the step before is multiplied, with the
+// DMAs spread between its MFMA groups behind sched_barrier fences, was
+// slower: the fp32 C2 gram 225 against 215 us, with 212 VGPRs against 136.)
 constexpr int DST = 4;               // ring stages
 constexpr int DTILE = GT * GK * 4;   // bytes of one operand tile (8 KiB)
 constexpr int DSTAGE = 2 * DTILE;    // A tile, then B tile
