@@ -1,13 +1,16 @@
-// Batched fp32 GEMM on gfx950 matrix cores (v_mfma_f32_32x32x2f32: exact
-// fp32 products, fp32 accumulation) with the epilogues of the recurrence's
-// closed form.  Used by the fp32 forward (prefill_f32.hip) and the backward
-// (vjp.hip).
+// Batched fp32 GEMM on gfx950 matrix cores (v_mfma_f32_16x16x4f32 and
+// v_mfma_f32_32x32x2f32: exact fp32 products, fp32 accumulation) with the
+// epilogues of the recurrence's closed form.  Used by the fp32 forward
+// (prefill_f32.hip) and the backward (vjp.hip).  Two kernels: the
+// direct-load kernel further down for operands contiguous along k or along
+// their rows (the common case), and this register-staged one for the rest.
 //
 //   C(m, n) = sum_k A(m, k) B(n, k),  batch b = (b / H, b % H):
 //   X(i, j) = X + (b / H) * sXo + (b % H) * sXi + i * sXr + j * sXc
 //
-// Workgroups of 256 threads own 128 x 128 output tiles, each wave a 64 x 64
-// block (2 x 2 MFMA blocks, 64 accumulators a lane).  K steps are 16 deep:
+// Register-staged kernel: workgroups of 256 threads own 128 x 128 output
+// tiles, each wave a 64 x 64 block (2 x 2 MFMA blocks of
+// v_mfma_f32_32x32x2f32, 64 accumulators a lane).  K steps are 16 deep:
 // the operands of step k + 1 are loaded into registers (16-byte loads where
 // the operand is contiguous along k or along its rows) while step k is
 // multiplied from LDS; LDS holds two steps, so one barrier a step suffices.

@@ -5,7 +5,7 @@
 //   ctx    = S V + (Q * d^r) rho                              [context]
 //   rho'   = rho * d^L + (Q * d^(L-r))^T V                     [state]
 // with r, c token offsets inside the interval.  Each product is a batched
-// fp32 GEMM on the matrix cores (bdh_gemm_f32.h: v_mfma_f32_32x32x2f32,
+// fp32 GEMM on the matrix cores (bdh_gemm_f32.h: v_mfma_f32_16x16x4f32,
 // exact fp32 products and fp32 accumulation), the masks and decay powers in
 // its epilogue or operand loads:
 //   gram     A = B = Q (rows t, k over N), epilogue tril(-1) * d^(r-c)

@@ -23,7 +23,7 @@
 //   grad_v += d^(L-t) (Q Gamma_{iv+1})        gemm P, then a scaled add
 //   grad_d += sum (L-t) d^(L-t) P V / sd + L d^L <rho_iv, Gamma_{iv+1}> / sd
 // and grad_rho0 = Gamma_0.
-// Every product is a batched fp32 GEMM on v_mfma_f32_32x32x2f32 (exact fp32
+// Every product is a batched fp32 GEMM on the fp32 MFMAs (exact fp32
 // products, fp32 accumulation; bdh_gemm_f32.h) with generic strides, so
 // transposed operands need no copy.  Reductions are per stream (f64) and then
 // per head in a fixed order: the result is deterministic.
