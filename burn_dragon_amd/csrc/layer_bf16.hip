@@ -265,6 +265,257 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
   for (int id = blockIdx.x; id < total; id += gridDim.x) gemm_tile<KIND>(g, lds, id);
 }
 
+// ---- GEMM X in two wave roles ---------------------------------------------
+// x = act(cur E_h) and q = rope(x) are 2 GB of stores per C5 layer against
+// 24 MB of operands: the launch is a write stream.  In layer_gemm_kernel a
+// tile's K loop waits for its loads with the one counter that also counts
+// the previous tile's stores (gfx9 has no separate store counter), so every
+// tile first drains 128 KB of stores.  Here one 1024-thread workgroup per CU
+// splits the work by wave:
+//   waves 0-7 (MFMA): load cur tiles through a 3-slot direct-load ring and
+//     multiply them with the workgroup's 128-latent encoder chunk, which
+//     stays in LDS for all its tiles (loaded once); per 128 x 128 tile they
+//     write act(x) in f32 to a staging tile.  They issue no stores, so their
+//     waits count their DMAs only.  They meet once per K step through an LDS
+//     counter rather than a workgroup barrier.
+//   waves 8-15 (store): per tile, read the staging tile, form x in bf16 and
+//     q = rope(x) (the f32 rotation in the reference's op order) and store
+//     both, 16 bytes a lane.  They issue no loads.
+// All waves pass two barriers per tile: G (the store waves have read the
+// previous staging tile) before the MFMA waves write it, and F (written)
+// before the store waves read it.  The product is computed transposed,
+// E_chunk cur^T, so each accumulator register of a lane holds 4 consecutive
+// latents of one token.  The workgroup owns one column tile (latent chunk)
+// and walks the row tiles in order, so at any time the workgroups write
+// neighbouring 256-byte pieces of the same rows.  Needs T % 128 == 0,
+// N % 128 == 0, 64 <= D <= 256 with D % 32 == 0, and at most one column tile
+// per CU (C5: 256 column tiles on 256 CUs).  Measured at C5 (GEMM X of
+// layer_gemm_kernel: 688 us): 766 us with 4 MFMA and 4 store waves and a
+// barrier per K step (the store waves, whose pieces took longer than a
+// step, held the barriers); 733 us with 8 store waves; 620 us without 64-bit
+// divisions in the loops; 601 us with 8 MFMA waves meeting through the LDS
+// counter and the store waves free between tiles.  An s_memtime trace of the
+// last form: ~1100 cycles per K step for 8 MFMAs a wave (the counter wait
+// ~340, one DMA issue ~240, fragment reads and MFMAs ~370), the store waves
+// idle ~60 % of a tile.
+constexpr int XR_T = 128;                      // tile edge (tokens and latents)
+constexpr int XR_EBLK = XR_T * BK * 2;         // bytes of one 32-deep block of 128 rows
+constexpr int XR_EMAX = (T256 / BK) * XR_EBLK; // encoder chunk, D <= 256
+constexpr int XR_RING = 3;
+constexpr int XR_STG = XR_T * XR_T * 4;        // f32 staging tile
+constexpr int XR_MW = 8;                       // MFMA waves (2 a SIMD: one's DMA issue and waits overlap the other's MFMAs)
+constexpr int XR_SW = 8;                       // store waves
+constexpr int XR_PC = 32 / XR_SW;              // 16-byte pieces of x (and of q) a store lane writes per tile
+constexpr int XR_LDS = XR_EMAX + XR_RING * XR_EBLK + XR_STG;
+
+// acc[mi][ni] += A[arow + 16 mi] x B[brow + 16 ni]^T over one 32-deep step
+// (4 x 2 MFMA blocks), fragment reads in assembly as mma_64x64_dsasm.
+__device__ __forceinline__ void mma_64x32_dsasm(const bf16_t* A, const bf16_t* B, int lane, int arow, int brow,
+                                                floatx4 (&acc)[4][2]) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  const uint32_t a = lds_addr(A) + (uint32_t)(2 * lds_off(arow + (lane & 15), lane >> 4));
+  const uint32_t b = lds_addr(B) + (uint32_t)(2 * lds_off(brow + (lane & 15), lane >> 4));
+  u32x4_t af[4], bf[2];
+  asm volatile("ds_read_b128 %0, %1 offset:0" : "=v"(bf[0]) : "v"(b));
+  asm volatile("ds_read_b128 %0, %1 offset:1024" : "=v"(bf[1]) : "v"(b));
+  asm volatile("ds_read_b128 %0, %1 offset:0" : "=v"(af[0]) : "v"(a));
+  asm volatile("ds_read_b128 %0, %1 offset:1024" : "=v"(af[1]) : "v"(a));
+  asm volatile("ds_read_b128 %0, %1 offset:2048" : "=v"(af[2]) : "v"(a));
+  asm volatile("ds_read_b128 %0, %1 offset:3072" : "=v"(af[3]) : "v"(a));
+  auto mm = [&](int mi, int ni) {
+    acc[mi][ni] = mfma16(__builtin_bit_cast(bf16x8, af[mi]), __builtin_bit_cast(bf16x8, bf[ni]), acc[mi][ni]);
+  };
+  asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(bf[0]), "+v"(bf[1]), "+v"(af[0]));
+  mm(0, 0);
+  mm(0, 1);
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[1]), "+v"(af[2]), "+v"(af[3]));
+#pragma unroll
+  for (int mi = 1; mi < 4; ++mi) {
+    mm(mi, 0);
+    mm(mi, 1);
+  }
+}
+
+// Byte offset of f32 staging element (t, n): 16-byte chunk n / 4 of the
+// 512-byte row t stored at chunk (n / 4) ^ (t & 15), so the MFMA waves' 16
+// rows a write and the store waves' rows fall on distinct banks.
+__device__ __forceinline__ uint32_t xr_stg(int t, int n) {
+  return (uint32_t)(t * 512 + ((((n >> 2) ^ (t & 15))) << 4) + 4 * (n & 3));
+}
+
+template <bool PLAIN>
+__global__ __launch_bounds__(64 * (XR_MW + XR_SW), 1) void layer_x_roles_kernel(LayerGemmArgs g, int rg_count) {
+  __shared__ __attribute__((aligned(16))) char lds[XR_LDS];
+  __shared__ uint32_t step_count;  // MFMA waves' arrivals at their K steps
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (tid == 0) step_count = 0;
+  __syncthreads();
+  const int ct = (int)(g.H * g.N / XR_T), mt = (int)(g.M / XR_T);
+  const int ctile = (int)blockIdx.x % ct, rg = (int)blockIdx.x / ct;
+  const int ntile = (mt - rg + rg_count - 1) / rg_count;  // row tiles rg, rg + rg_count, ...
+  const int nk = (int)(g.D / BK);
+  const int J = ntile * nk;  // K steps of the workgroup
+  const int64_t c0 = (int64_t)ctile * XR_T, h = c0 / g.N, n0 = c0 - h * g.N;
+  char* const E = lds;
+  char* const ring = lds + XR_EMAX;
+  char* const stg = lds + XR_EMAX + XR_RING * XR_EBLK;
+  const int gq = lane >> 4, li = lane & 15;
+
+  if (w < XR_MW) {
+    // ---- MFMA waves: wave w owns latents 64 (w / 4) .. + 63 and tokens
+    // 32 (w % 4) .. + 31 of the tile ----
+    const int wm = w >> 2, wt = w & 3;
+    const uint32_t lE = lds_addr(E), lR = lds_addr(ring);
+    // DMA lane offsets: instruction i of a 128-row block covers rows 16 i ..
+    // 16 i + 15, lane l row 16 i + l / 4, LDS chunk l & 3 = global chunk
+    // (l & 3) ^ ((row >> 1) & 3) (the lds_off swizzle).
+    auto src = [&](int i) {
+      const int r = 16 * i + (lane >> 2);
+      const int c = (lane & 3) ^ ((r >> 1) & 3);
+      return (uint32_t)(r * g.D * 2 + c * 16);
+    };
+    const bf16_t* Eg = g.b + c0 * g.D;
+    for (int idx = w; idx < nk * 8; idx += XR_MW) {
+      const int sblk = idx >> 3, i = idx & 7;
+      dma16(Eg, src(i) + (uint32_t)(sblk * 64), lE + (uint32_t)(sblk * XR_EBLK + i * 1024));
+    }
+    const uint32_t cs0 = src(w);  // one DMA instruction a wave and step
+    // The next step to fetch: its cur rows, k block and ring slot, advanced
+    // step by step (no divisions in the loop).
+    const bf16_t* cg = g.a + (int64_t)rg * XR_T * g.D;
+    const int64_t cstep = (int64_t)rg_count * XR_T * g.D;
+    int isk = 0, islot = 0, issued = 0;
+    auto issue = [&]() {
+      const uint32_t d = lR + (uint32_t)(islot * XR_EBLK);
+      dma16(cg, cs0 + (uint32_t)(isk * 64), d + (uint32_t)(w * 1024));
+      ++issued;
+      islot = islot == XR_RING - 1 ? 0 : islot + 1;
+      if (++isk == nk) {
+        isk = 0;
+        cg += cstep;
+      }
+    };
+    float mk[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mk[mi][r] = (!PLAIN && g.mask) ? g.mask[n0 + 64 * wm + 16 * mi + 4 * gq + r] : 1.0f;
+    const float th = g.relu_th;
+    floatx4 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = zero4();
+    issue();
+    if (J > 1) issue();
+    int slot = 0;
+    const uint32_t sc = lds_addr(&step_count);
+    for (int j = 0, sk = 0; j < J; ++j) {
+      // Step j has landed once only the DMA of step j + 1 (1 a wave), if
+      // issued, is in flight; the encoder chunk's DMAs are older.  Then the
+      // MFMA waves meet through an LDS counter, not a workgroup barrier, so
+      // that the store waves run free between tiles: each adds 1 and waits
+      // for 8 (j + 1).  Past it every MFMA wave's DMAs of step j have landed
+      // and every one has finished step j - 1's LDS reads.  The wait is
+      // bounded (about 2^20 polls), so it ends whatever happens.
+      if (j + 1 < J) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (lane == 0) asm volatile("ds_add_u32 %0, %1" ::"v"(sc), "v"(1u) : "memory");
+      const uint32_t target = (uint32_t)(XR_MW * (j + 1));
+      for (int poll = 0; poll < (1 << 20); ++poll) {
+        uint32_t v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sc) : "memory");
+        if ((uint32_t)__builtin_amdgcn_readfirstlane((int)v) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      // Into the slot of step j - 1, which every MFMA wave has finished reading.
+      if (issued < J) issue();
+      mma_64x32_dsasm(reinterpret_cast<const bf16_t*>(E + sk * XR_EBLK),
+                      reinterpret_cast<const bf16_t*>(ring + slot * XR_EBLK), lane, 64 * wm, 32 * wt, acc);
+      slot = slot == XR_RING - 1 ? 0 : slot + 1;
+      if (++sk == nk) {
+        sk = 0;
+        // Barrier G: the store waves have read the previous tile's staging.
+        asm volatile("s_barrier" ::: "memory");
+        // The tile's act(x), f32, into the staging tile:
+        // block (mi, ni), register r is latent 64 wm + 16 mi + 4 gq + r of
+        // token 32 wt + 16 ni + li.
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < 2; ++ni) {
+            const int t = 32 * wt + 16 * ni + li, n = 64 * wm + 16 * mi + 4 * gq;
+            float4 v;
+            if (PLAIN) {
+              v = make_float4(fmaxf(acc[mi][ni][0], 0.0f), fmaxf(acc[mi][ni][1], 0.0f), fmaxf(acc[mi][ni][2], 0.0f),
+                              fmaxf(acc[mi][ni][3], 0.0f));
+            } else {
+              v = make_float4(lowrank_act(acc[mi][ni][0], th, mk[mi][0]), lowrank_act(acc[mi][ni][1], th, mk[mi][1]),
+                              lowrank_act(acc[mi][ni][2], th, mk[mi][2]), lowrank_act(acc[mi][ni][3], th, mk[mi][3]));
+            }
+            *reinterpret_cast<float4*>(stg + xr_stg(t, n)) = v;
+            acc[mi][ni] = zero4();
+          }
+        // Barrier F: the staging tile is written.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+    }
+    return;
+  }
+
+  // ---- store waves ----
+  const int sw = w - XR_MW;
+  // Piece u (0 .. XR_PC - 1) of a tile: token row (128 / XR_SW) sw + 4 u + gq,
+  // latents 8 li .. 8 li + 7.
+  float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (g.q) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fq[j] = g.freqs[n0 + 8 * li + 2 * j];
+  }
+  int64_t obase = 0, pbase = 0;  // of the staged tile: offset of its token 0, that token's position
+  auto store_piece = [&](int u) {
+    const int tl = (XR_T / XR_SW) * sw + 4 * u + gq;
+    const int64_t o = obase + (int64_t)tl * g.N;
+    const int64_t t = pbase + tl;
+    const float4 lo = *reinterpret_cast<const float4*>(stg + xr_stg(tl, 8 * li));
+    const float4 hi = *reinterpret_cast<const float4*>(stg + xr_stg(tl, 8 * li + 4));
+    const float r[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    __builtin_nontemporal_store(u32x4{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]),
+                                      pack_bf16x2(r[6], r[7])},
+                                reinterpret_cast<u32x4*>(g.xy + o));
+    if (g.q) {
+      // Phase frac(p f) in the reference's f32 op order, cos / sin by
+      // v_cos_f32 / v_sin_f32 (argument in revolutions); the rotation in the
+      // op order of attention.rs:488-501 (as layer_gemm_kernel<G_X>).
+      const float p = (float)(g.fixed ? g.pos0 : g.pos0 + t);
+      float qv[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float fr = rope_frac(p, fq[j]);
+        rope_pair_exact(r[2 * j], r[2 * j + 1], __builtin_amdgcn_cosf(fr), __builtin_amdgcn_sinf(fr), qv[2 * j],
+                        qv[2 * j + 1]);
+      }
+      __builtin_nontemporal_store(u32x4{pack_bf16x2(qv[0], qv[1]), pack_bf16x2(qv[2], qv[3]),
+                                        pack_bf16x2(qv[4], qv[5]), pack_bf16x2(qv[6], qv[7])},
+                                  reinterpret_cast<u32x4*>(g.q + o));
+    }
+  };
+  // Per tile: barriers G and F (as the MFMA waves), then the tile's pieces
+  // read from staging, formed and stored, before the next G.
+  int64_t row0 = (int64_t)rg * XR_T;  // first token row (b * T + t) of the tile
+  for (int i = 0; i < ntile; ++i) {
+    asm volatile("s_barrier" ::: "memory");  // G
+    asm volatile("s_barrier" ::: "memory");  // F: the staging tile of tile i is written
+    // A tile lies inside one sequence (T % 128 == 0).
+    const int64_t bb = row0 / g.T, t0 = row0 - bb * g.T;
+    obase = ((bb * g.H + h) * g.T + t0) * g.N + n0 + 8 * li;
+    pbase = t0;
+    row0 += (int64_t)rg_count * XR_T;
+#pragma unroll
+    for (int u = 0; u < XR_PC; ++u) store_piece(u);
+  }
+}
+
 // ---- GEMM Y fused into GEMM Z --------------------------------------------
 // With T a multiple of 256 and D <= 256 the layer never writes y.  One
 // workgroup (8 waves, one per CU) owns a 256-token tile (one sequence) and a
@@ -822,6 +1073,32 @@ hipError_t launch_gemm(const LayerGemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Row-tile groups of the two-role GEMM X (layer_x_roles_kernel), or 0 where
+// the shape needs layer_gemm_kernel<G_X>: x wanted in f32 (the decode step),
+// few rows, T or N not a multiple of 128, D not a multiple of 32, under 64
+// or above 256, or more 128-latent column tiles than CUs.  A workgroup per column
+// tile and group; the groups split the row tiles.
+int x_roles_groups(const LayerGemmArgs& g) {
+  if (g.xf || g.M <= SK_MAXM || g.T % XR_T != 0 || g.N % XR_T != 0 || g.D % BK != 0 || g.D < 2 * BK ||
+      g.D > T256)
+    return 0;
+  const int64_t ct = g.H * g.N / XR_T, mt = g.M / XR_T, cus = device_cus();
+  if (ct > cus) return 0;
+  const int64_t r = cus / ct;
+  return (int)(r < mt ? r : mt);
+}
+
+hipError_t launch_x(const LayerGemmArgs& g, hipStream_t st) {
+  const int groups = x_roles_groups(g);
+  if (groups == 0) return launch_gemm<G_X>(g, st);
+  const dim3 grid((unsigned)(g.H * g.N / XR_T * groups));
+  if (g.relu_th == 0.0f && g.mask == nullptr)
+    hipLaunchKernelGGL(layer_x_roles_kernel<true>, grid, dim3(64 * (XR_MW + XR_SW)), 0, st, g, groups);
+  else
+    hipLaunchKernelGGL(layer_x_roles_kernel<false>, grid, dim3(64 * (XR_MW + XR_SW)), 0, st, g, groups);
+  return hipGetLastError();
+}
+
 // Split count of the fused Y + Z launch over the 128-latent chunks, or 0
 // where the shape needs GEMM Y and GEMM Z apart: T a multiple of 256 (a
 // token tile inside one sequence), D a multiple of 64 up to 256 (the z tile),
@@ -1032,7 +1309,7 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
   g.fixed = a.fixed;
   g.relu_th = a.relu_th;
   g.mask = a.mask;
-  BDH_HIP_TRY(launch_gemm<G_X>(g, st));
+  BDH_HIP_TRY(launch_x(g, st));
   g.q = nullptr;
   g.xf = nullptr;
 
