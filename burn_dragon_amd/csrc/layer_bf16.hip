@@ -265,46 +265,60 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
   for (int id = blockIdx.x; id < total; id += gridDim.x) gemm_tile<KIND>(g, lds, id);
 }
 
-// ---- GEMM X in two wave roles ---------------------------------------------
+// ---- GEMM X in wave roles -------------------------------------------------
 // x = act(cur E_h) and q = rope(x) are 2 GB of stores per C5 layer against
 // 24 MB of operands: the launch is a write stream.  In layer_gemm_kernel a
 // tile's K loop waits for its loads with the one counter that also counts
 // the previous tile's stores (gfx9 has no separate store counter), so every
 // tile first drains 128 KB of stores.  Here one 1024-thread workgroup per CU
-// splits the work by wave:
-//   waves 0-7 (MFMA): load cur tiles through a 3-slot direct-load ring and
-//     multiply them with the workgroup's 128-latent encoder chunk, which
-//     stays in LDS for all its tiles (loaded once); per 128 x 128 tile they
-//     write act(x) in f32 to a staging tile.  They issue no stores, so their
-//     waits count their DMAs only.  They meet once per K step through an LDS
-//     counter rather than a workgroup barrier.
+// splits the work by wave, and no wave both loads and stores:
+//   waves 0-3 (MFMA): multiply each 32-deep step of the cur tile, taken from
+//     a 3-slot LDS ring, with the workgroup's 128-latent encoder chunk, which
+//     stays in LDS for all its tiles; per 128 x 128 tile they write act(x)
+//     in f32 to a staging tile.  No global memory access at all (the
+//     optional latent mask aside).
+//   waves 4-7 (DMA): fetch the encoder chunk once and then each step's cur
+//     rows straight into the ring (global_load_lds_dwordx4), waiting only
+//     for their own DMAs.
 //   waves 8-15 (store): per tile, read the staging tile, form x in bf16 and
 //     q = rope(x) (the f32 rotation in the reference's op order) and store
-//     both, 16 bytes a lane.  They issue no loads.
+//     both, 16 bytes a lane.
+// MFMA and DMA waves hand the ring over through per-wave progress counters
+// in LDS (steps landed, per DMA wave; steps read, per MFMA wave), not
+// workgroup barriers: a DMA wave refills a slot once every MFMA wave has
+// read it, an MFMA wave multiplies a step once every DMA wave has landed it.
 // All waves pass two barriers per tile: G (the store waves have read the
 // previous staging tile) before the MFMA waves write it, and F (written)
-// before the store waves read it.  The product is computed transposed,
-// E_chunk cur^T, so each accumulator register of a lane holds 4 consecutive
-// latents of one token.  The workgroup owns one column tile (latent chunk)
-// and walks the row tiles in order, so at any time the workgroups write
-// neighbouring 256-byte pieces of the same rows.  Needs T % 128 == 0,
-// N % 128 == 0, 64 <= D <= 256 with D % 32 == 0, and at most one column tile
-// per CU (C5: 256 column tiles on 256 CUs).  Measured at C5 (GEMM X of
-// layer_gemm_kernel: 688 us): 766 us with 4 MFMA and 4 store waves and a
-// barrier per K step (the store waves, whose pieces took longer than a
-// step, held the barriers); 733 us with 8 store waves; 620 us without 64-bit
-// divisions in the loops; 601 us with 8 MFMA waves meeting through the LDS
-// counter and the store waves free between tiles.  An s_memtime trace of the
-// last form: ~1100 cycles per K step for 8 MFMAs a wave (the counter wait
-// ~340, one DMA issue ~240, fragment reads and MFMAs ~370), the store waves
-// idle ~60 % of a tile.
+// before the store waves read it; a DMA wave passes tile i's two barriers
+// in step (i + 1) nk + 2, once it knows that the MFMA waves have finished
+// tile i and before it needs anything of tile i + 1 from them (a CPU model
+// of the protocol checked every interleaving it sampled for 1-6 tiles and
+// 2-8 steps: no deadlock, no slot read stale).
+// The product is computed transposed, E_chunk cur^T, so each accumulator
+// register of a lane holds 4 consecutive latents of one token.  The
+// workgroup owns one column tile (latent chunk) and walks the row tiles in
+// order, so at any time the workgroups write neighbouring 256-byte pieces of
+// the same rows.  Needs T % 128 == 0, N % 128 == 0, 64 <= D <= 256 with
+// D % 32 == 0, and at most one column tile per CU (C5: 256 column tiles on
+// 256 CUs).  Measured at C5 (GEMM X of layer_gemm_kernel: 688 us): 766 us
+// with 4 MFMA waves that also issued the DMAs, 4 store waves and a barrier
+// per K step (the store waves held the barriers); 620 us with 8 store waves
+// and no 64-bit divisions in the loops; 601 us with 8 MFMA waves meeting
+// through an LDS counter and the store waves free between tiles; 540 us
+// with the DMAs in waves of their own; 520 us with polls skipped where an
+// earlier read already showed the step.  An s_memtime trace at 540 us: a K
+// step ~970 cycles for an MFMA wave (16 MFMAs and their fragment reads
+// ~520, the counter poll ~270), a tile ~9.9 k cycles, the store waves idle
+// about half of it.
 constexpr int XR_T = 128;                      // tile edge (tokens and latents)
 constexpr int XR_EBLK = XR_T * BK * 2;         // bytes of one 32-deep block of 128 rows
 constexpr int XR_EMAX = (T256 / BK) * XR_EBLK; // encoder chunk, D <= 256
 constexpr int XR_RING = 3;
 constexpr int XR_STG = XR_T * XR_T * 4;        // f32 staging tile
-constexpr int XR_MW = 8;                       // MFMA waves (2 a SIMD: one's DMA issue and waits overlap the other's MFMAs)
+constexpr int XR_MW = 4;                       // MFMA waves
+constexpr int XR_DW = 4;                       // DMA waves
 constexpr int XR_SW = 8;                       // store waves
+static_assert(XR_MW == 4 && XR_DW == 4, "the progress counters are read 4 at a time");
 constexpr int XR_PC = 32 / XR_SW;              // 16-byte pieces of x (and of q) a store lane writes per tile
 constexpr int XR_LDS = XR_EMAX + XR_RING * XR_EBLK + XR_STG;
 
@@ -343,12 +357,34 @@ __device__ __forceinline__ uint32_t xr_stg(int t, int n) {
   return (uint32_t)(t * 512 + ((((n >> 2) ^ (t & 15))) << 4) + 4 * (n & 3));
 }
 
+// Per-wave progress counters in LDS, each written by its one wave: a wave
+// waits until the least of a group's 4 counters (one 16-byte read at byte
+// address a) reaches target.  A poll, then a short sleep; bounded (about
+// 2^20 polls, tens of milliseconds), so it ends whatever happens; the
+// protocol's waits end within a few K steps.
+// seen: the least value this wave last read (counters only grow), so a wait
+// that an earlier poll already satisfied reads nothing.
+__device__ __forceinline__ void xr_wait_min4(uint32_t a, uint32_t target, uint32_t& seen) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  for (int poll = 0; poll < (1 << 20) && seen < target; ++poll) {
+    if (poll > 0) __builtin_amdgcn_s_sleep(1);
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+    seen = (uint32_t)__builtin_amdgcn_readfirstlane((int)min(min(v.x, v.y), min(v.z, v.w)));
+  }
+}
+__device__ __forceinline__ void xr_count_set(uint32_t a, uint32_t value, int lane) {
+  if (lane == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(value) : "memory");
+}
+
 template <bool PLAIN>
-__global__ __launch_bounds__(64 * (XR_MW + XR_SW), 1) void layer_x_roles_kernel(LayerGemmArgs g, int rg_count) {
+__global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles_kernel(LayerGemmArgs g, int rg_count) {
   __shared__ __attribute__((aligned(16))) char lds[XR_LDS];
-  __shared__ uint32_t step_count;  // MFMA waves' arrivals at their K steps
+  // counts[0..3]: K steps whose DMAs have landed, per DMA wave;
+  // counts[4..7]: K steps finished reading, per MFMA wave.
+  __shared__ __attribute__((aligned(16))) uint32_t counts[8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  if (tid == 0) step_count = 0;
+  if (tid < 8) counts[tid] = 0;
   __syncthreads();
   const int ct = (int)(g.H * g.N / XR_T), mt = (int)(g.M / XR_T);
   const int ctile = (int)blockIdx.x % ct, rg = (int)blockIdx.x / ct;
@@ -360,91 +396,45 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_SW), 1) void layer_x_roles_kernel(
   char* const ring = lds + XR_EMAX;
   char* const stg = lds + XR_EMAX + XR_RING * XR_EBLK;
   const int gq = lane >> 4, li = lane & 15;
+  const uint32_t landed = lds_addr(&counts[0]), consumed = lds_addr(&counts[4]);
 
   if (w < XR_MW) {
-    // ---- MFMA waves: wave w owns latents 64 (w / 4) .. + 63 and tokens
-    // 32 (w % 4) .. + 31 of the tile ----
-    const int wm = w >> 2, wt = w & 3;
-    const uint32_t lE = lds_addr(E), lR = lds_addr(ring);
-    // DMA lane offsets: instruction i of a 128-row block covers rows 16 i ..
-    // 16 i + 15, lane l row 16 i + l / 4, LDS chunk l & 3 = global chunk
-    // (l & 3) ^ ((row >> 1) & 3) (the lds_off swizzle).
-    auto src = [&](int i) {
-      const int r = 16 * i + (lane >> 2);
-      const int c = (lane & 3) ^ ((r >> 1) & 3);
-      return (uint32_t)(r * g.D * 2 + c * 16);
-    };
-    const bf16_t* Eg = g.b + c0 * g.D;
-    for (int idx = w; idx < nk * 8; idx += XR_MW) {
-      const int sblk = idx >> 3, i = idx & 7;
-      dma16(Eg, src(i) + (uint32_t)(sblk * 64), lE + (uint32_t)(sblk * XR_EBLK + i * 1024));
-    }
-    const uint32_t cs0 = src(w);  // one DMA instruction a wave and step
-    // The next step to fetch: its cur rows, k block and ring slot, advanced
-    // step by step (no divisions in the loop).
-    const bf16_t* cg = g.a + (int64_t)rg * XR_T * g.D;
-    const int64_t cstep = (int64_t)rg_count * XR_T * g.D;
-    int isk = 0, islot = 0, issued = 0;
-    auto issue = [&]() {
-      const uint32_t d = lR + (uint32_t)(islot * XR_EBLK);
-      dma16(cg, cs0 + (uint32_t)(isk * 64), d + (uint32_t)(w * 1024));
-      ++issued;
-      islot = islot == XR_RING - 1 ? 0 : islot + 1;
-      if (++isk == nk) {
-        isk = 0;
-        cg += cstep;
-      }
-    };
+    // ---- MFMA waves: wave w owns latents 64 (w / 2) .. + 63 and tokens
+    // 64 (w % 2) .. + 63 of the tile ----
+    const int wm = w >> 1, wt = w & 1;
     float mk[4][4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mk[mi][r] = (!PLAIN && g.mask) ? g.mask[n0 + 64 * wm + 16 * mi + 4 * gq + r] : 1.0f;
     const float th = g.relu_th;
-    floatx4 acc[4][2];
+    floatx4 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = zero4();
-    issue();
-    if (J > 1) issue();
+      for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
     int slot = 0;
-    const uint32_t sc = lds_addr(&step_count);
+    uint32_t seen = 0;
     for (int j = 0, sk = 0; j < J; ++j) {
-      // Step j has landed once only the DMA of step j + 1 (1 a wave), if
-      // issued, is in flight; the encoder chunk's DMAs are older.  Then the
-      // MFMA waves meet through an LDS counter, not a workgroup barrier, so
-      // that the store waves run free between tiles: each adds 1 and waits
-      // for 8 (j + 1).  Past it every MFMA wave's DMAs of step j have landed
-      // and every one has finished step j - 1's LDS reads.  The wait is
-      // bounded (about 2^20 polls), so it ends whatever happens.
-      if (j + 1 < J) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      if (lane == 0) asm volatile("ds_add_u32 %0, %1" ::"v"(sc), "v"(1u) : "memory");
-      const uint32_t target = (uint32_t)(XR_MW * (j + 1));
-      for (int poll = 0; poll < (1 << 20); ++poll) {
-        uint32_t v;
-        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sc) : "memory");
-        if ((uint32_t)__builtin_amdgcn_readfirstlane((int)v) >= target) break;
-        __builtin_amdgcn_s_sleep(1);
-      }
-      // Into the slot of step j - 1, which every MFMA wave has finished reading.
-      if (issued < J) issue();
-      mma_64x32_dsasm(reinterpret_cast<const bf16_t*>(E + sk * XR_EBLK),
-                      reinterpret_cast<const bf16_t*>(ring + slot * XR_EBLK), lane, 64 * wm, 32 * wt, acc);
+      // Step j (and, before step 0, the encoder chunk) has landed.
+      xr_wait_min4(landed, (uint32_t)(j + 1), seen);
+      mma_64x64_dsasm(reinterpret_cast<const bf16_t*>(E + sk * XR_EBLK),
+                      reinterpret_cast<const bf16_t*>(ring + slot * XR_EBLK), lane, 64 * wm, 64 * wt, acc);
+      // The fragment reads are complete (waited inside): the slot is free.
+      xr_count_set(consumed + 4 * w, (uint32_t)(j + 1), lane);
       slot = slot == XR_RING - 1 ? 0 : slot + 1;
       if (++sk == nk) {
         sk = 0;
         // Barrier G: the store waves have read the previous tile's staging.
         asm volatile("s_barrier" ::: "memory");
-        // The tile's act(x), f32, into the staging tile:
-        // block (mi, ni), register r is latent 64 wm + 16 mi + 4 gq + r of
-        // token 32 wt + 16 ni + li.
+        // The tile's act(x), f32, into the staging tile: block (mi, ni),
+        // register r is latent 64 wm + 16 mi + 4 gq + r of token
+        // 64 wt + 16 ni + li.
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-          for (int ni = 0; ni < 2; ++ni) {
-            const int t = 32 * wt + 16 * ni + li, n = 64 * wm + 16 * mi + 4 * gq;
+          for (int ni = 0; ni < 4; ++ni) {
+            const int t = 64 * wt + 16 * ni + li, n = 64 * wm + 16 * mi + 4 * gq;
             float4 v;
             if (PLAIN) {
               v = make_float4(fmaxf(acc[mi][ni][0], 0.0f), fmaxf(acc[mi][ni][1], 0.0f), fmaxf(acc[mi][ni][2], 0.0f),
@@ -463,8 +453,69 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_SW), 1) void layer_x_roles_kernel(
     return;
   }
 
+  if (w < XR_MW + XR_DW) {
+    // ---- DMA waves: wave dw issues instructions dw and dw + 4 of each
+    // step's 8 (cur rows 16 i .. 16 i + 15) ----
+    const int dw = w - XR_MW;
+    const uint32_t lE = lds_addr(E), lR = lds_addr(ring);
+    // Instruction i of a 128-row block covers rows 16 i .. 16 i + 15, lane l
+    // row 16 i + l / 4, LDS chunk l & 3 = global chunk (l & 3) ^ ((row >> 1)
+    // & 3) (the lds_off swizzle).
+    auto src = [&](int i) {
+      const int r = 16 * i + (lane >> 2);
+      const int c = (lane & 3) ^ ((r >> 1) & 3);
+      return (uint32_t)(r * g.D * 2 + c * 16);
+    };
+    const bf16_t* Eg = g.b + c0 * g.D;
+    for (int idx = dw; idx < nk * 8; idx += XR_DW) {
+      const int sblk = idx >> 3, i = idx & 7;
+      dma16(Eg, src(i) + (uint32_t)(sblk * 64), lE + (uint32_t)(sblk * XR_EBLK + i * 1024));
+    }
+    const uint32_t cs0 = src(dw), cs1 = src(dw + XR_DW);
+    const bf16_t* cg = g.a + (int64_t)rg * XR_T * g.D;
+    const int64_t cstep = (int64_t)rg_count * XR_T * g.D;
+    // Tile barriers G and F: the MFMA waves reach tile i's once they have
+    // finished its last step, (i + 1) nk - 1.  This wave passes them in
+    // step j = (i + 1) nk + 2, right after learning that: until then the
+    // MFMA waves need no step it has not signalled (it signals step j - 1 in
+    // step j), and from step j + 1 on it waits for steps of tile i + 1.
+    int tiles_met = 0;
+    int sk = 0, slot = 0;
+    uint32_t seen = 0;
+    for (int j = 0; j < J; ++j) {
+      // Slot j % 3 held step j - 3: free once every MFMA wave has read it.
+      if (j >= XR_RING) xr_wait_min4(consumed, (uint32_t)(j - XR_RING + 1), seen);
+      if (tiles_met < ntile && j == (tiles_met + 1) * nk + 2) {
+        asm volatile("s_barrier" ::: "memory");  // G
+        asm volatile("s_barrier" ::: "memory");  // F
+        ++tiles_met;
+      }
+      const uint32_t d = lR + (uint32_t)(slot * XR_EBLK);
+      dma16(cg, cs0 + (uint32_t)(sk * 64), d + (uint32_t)(dw * 1024));
+      dma16(cg, cs1 + (uint32_t)(sk * 64), d + (uint32_t)((dw + XR_DW) * 1024));
+      slot = slot == XR_RING - 1 ? 0 : slot + 1;
+      if (++sk == nk) {
+        sk = 0;
+        cg += cstep;
+      }
+      // Step j - 1 (this wave's part; with step 0 the encoder chunk) has
+      // landed once only step j's 2 DMAs are in flight.
+      if (j > 0) {
+        asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        xr_count_set(landed + 4 * dw, (uint32_t)j, lane);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    xr_count_set(landed + 4 * dw, (uint32_t)J, lane);  // step J - 1
+    for (; tiles_met < ntile; ++tiles_met) {
+      asm volatile("s_barrier" ::: "memory");  // G
+      asm volatile("s_barrier" ::: "memory");  // F
+    }
+    return;
+  }
+
   // ---- store waves ----
-  const int sw = w - XR_MW;
+  const int sw = w - XR_MW - XR_DW;
   // Piece u (0 .. XR_PC - 1) of a tile: token row (128 / XR_SW) sw + 4 u + gq,
   // latents 8 li .. 8 li + 7.
   float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1093,9 +1144,9 @@ hipError_t launch_x(const LayerGemmArgs& g, hipStream_t st) {
   if (groups == 0) return launch_gemm<G_X>(g, st);
   const dim3 grid((unsigned)(g.H * g.N / XR_T * groups));
   if (g.relu_th == 0.0f && g.mask == nullptr)
-    hipLaunchKernelGGL(layer_x_roles_kernel<true>, grid, dim3(64 * (XR_MW + XR_SW)), 0, st, g, groups);
+    hipLaunchKernelGGL(layer_x_roles_kernel<true>, grid, dim3(64 * (XR_MW + XR_DW + XR_SW)), 0, st, g, groups);
   else
-    hipLaunchKernelGGL(layer_x_roles_kernel<false>, grid, dim3(64 * (XR_MW + XR_SW)), 0, st, g, groups);
+    hipLaunchKernelGGL(layer_x_roles_kernel<false>, grid, dim3(64 * (XR_MW + XR_DW + XR_SW)), 0, st, g, groups);
   return hipGetLastError();
 }
 
