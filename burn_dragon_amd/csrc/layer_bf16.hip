@@ -291,9 +291,9 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
 // previous staging tile) before the MFMA waves write it, and F (written)
 // before the store waves read it; a DMA wave passes tile i's two barriers
 // in step (i + 1) nk + 2, once it knows that the MFMA waves have finished
-// tile i and before it needs anything of tile i + 1 from them (a CPU model
-// of the protocol checked every interleaving it sampled for 1-6 tiles and
-// 2-8 steps: no deadlock, no slot read stale).
+// tile i and before it needs anything of tile i + 1 from them
+// (tests/test_x_roles_protocol.py models the protocol on the CPU: random
+// interleavings finish with no slot read stale).
 // The product is computed transposed, E_chunk cur^T, so each accumulator
 // register of a lane holds 4 consecutive latents of one token.  The
 // workgroup owns one column tile (latent chunk) and walks the row tiles in
@@ -309,7 +309,10 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
 // earlier read already showed the step.  An s_memtime trace at 540 us: a K
 // step ~970 cycles for an MFMA wave (16 MFMAs and their fragment reads
 // ~520, the counter poll ~270), a tile ~9.9 k cycles, the store waves idle
-// about half of it.
+// about half of it.  Slower, not kept: the poll issued with the step's
+// fragment reads, the MFMAs after all of them (538 us); the DMA waves
+// passing the tile barriers right after the next tile's first step had
+// landed (vmcnt(0) there; 576 us with both).
 constexpr int XR_T = 128;                      // tile edge (tokens and latents)
 constexpr int XR_EBLK = XR_T * BK * 2;         // bytes of one 32-deep block of 128 rows
 constexpr int XR_EMAX = (T256 / BK) * XR_EBLK; // encoder chunk, D <= 256
