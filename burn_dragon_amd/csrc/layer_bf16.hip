@@ -283,17 +283,15 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
 //   waves 8-15 (store): per tile, read the staging tile, form x in bf16 and
 //     q = rope(x) (the f32 rotation in the reference's op order) and store
 //     both, 16 bytes a lane.
-// MFMA and DMA waves hand the ring over through per-wave progress counters
-// in LDS (steps landed, per DMA wave; steps read, per MFMA wave), not
-// workgroup barriers: a DMA wave refills a slot once every MFMA wave has
-// read it, an MFMA wave multiplies a step once every DMA wave has landed it.
-// All waves pass two barriers per tile: G (the store waves have read the
-// previous staging tile) before the MFMA waves write it, and F (written)
-// before the store waves read it; a DMA wave passes tile i's two barriers
-// in step (i + 1) nk + 2, once it knows that the MFMA waves have finished
-// tile i and before it needs anything of tile i + 1 from them
+// The waves hand work over through per-wave progress counters in LDS, not
+// workgroup barriers: steps landed (per DMA wave), steps read (per MFMA
+// wave), tiles staged (per MFMA wave), tiles read from staging (per store
+// wave).  A DMA wave refills a ring slot once every MFMA wave has read it;
+// an MFMA wave multiplies a step once every DMA wave has landed it, and
+// writes a tile's staging once every store wave has read the previous one;
+// a store wave reads a tile once every MFMA wave has staged it
 // (tests/test_x_roles_protocol.py models the protocol on the CPU: random
-// interleavings finish with no slot read stale).
+// interleavings finish with no slot or staging part read stale).
 // The product is computed transposed, E_chunk cur^T, so each accumulator
 // register of a lane holds 4 consecutive latents of one token.  The
 // workgroup owns one column tile (latent chunk) and walks the row tiles in
@@ -306,13 +304,16 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
 // and no 64-bit divisions in the loops; 601 us with 8 MFMA waves meeting
 // through an LDS counter and the store waves free between tiles; 540 us
 // with the DMAs in waves of their own; 520 us with polls skipped where an
-// earlier read already showed the step.  An s_memtime trace at 540 us: a K
-// step ~970 cycles for an MFMA wave (16 MFMAs and their fragment reads
-// ~520, the counter poll ~270), a tile ~9.9 k cycles, the store waves idle
-// about half of it.  Slower, not kept: the poll issued with the step's
+// earlier read already showed the step; 512 us with counters instead of the
+// two workgroup barriers per tile that all waves passed before.  An
+// s_memtime trace at 512 us: a K step ~920 cycles for an MFMA wave (16
+// MFMAs and their fragment reads ~540, the counter poll ~220), a tile ~9.2 k
+// cycles, the store waves idle about half of it.  Slower, not kept: the poll issued with the step's
 // fragment reads, the MFMAs after all of them (538 us); the DMA waves
 // passing the tile barriers right after the next tile's first step had
-// landed (vmcnt(0) there; 576 us with both).
+// landed (vmcnt(0) there; 576 us with both); the landed counters read behind
+// each step's MFMAs for the next step (523 us: the DMA waves, one step
+// ahead, had rarely signalled it by then).
 constexpr int XR_T = 128;                      // tile edge (tokens and latents)
 constexpr int XR_EBLK = XR_T * BK * 2;         // bytes of one 32-deep block of 128 rows
 constexpr int XR_EMAX = (T256 / BK) * XR_EBLK; // encoder chunk, D <= 256
@@ -366,14 +367,22 @@ __device__ __forceinline__ uint32_t xr_stg(int t, int n) {
 // 2^20 polls, tens of milliseconds), so it ends whatever happens; the
 // protocol's waits end within a few K steps.
 // seen: the least value this wave last read (counters only grow), so a wait
-// that an earlier poll already satisfied reads nothing.
-__device__ __forceinline__ void xr_wait_min4(uint32_t a, uint32_t target, uint32_t& seen) {
+// that an earlier poll already satisfied reads nothing.  N = 4 or 8
+// counters, 16-byte aligned.
+template <int N>
+__device__ __forceinline__ void xr_wait_min(uint32_t a, uint32_t target, uint32_t& seen) {
   typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
   for (int poll = 0; poll < (1 << 20) && seen < target; ++poll) {
     if (poll > 0) __builtin_amdgcn_s_sleep(1);
-    u32x4_t v;
-    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
-    seen = (uint32_t)__builtin_amdgcn_readfirstlane((int)min(min(v.x, v.y), min(v.z, v.w)));
+    u32x4_t v, u = u32x4_t{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+    if (N == 8) {
+      asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                   : "=&v"(v), "=&v"(u) : "v"(a) : "memory");
+    } else {
+      asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+    }
+    const uint32_t m = min(min(min(v.x, v.y), min(v.z, v.w)), min(min(u.x, u.y), min(u.z, u.w)));
+    seen = (uint32_t)__builtin_amdgcn_readfirstlane((int)m);
   }
 }
 __device__ __forceinline__ void xr_count_set(uint32_t a, uint32_t value, int lane) {
@@ -383,11 +392,12 @@ __device__ __forceinline__ void xr_count_set(uint32_t a, uint32_t value, int lan
 template <bool PLAIN>
 __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles_kernel(LayerGemmArgs g, int rg_count) {
   __shared__ __attribute__((aligned(16))) char lds[XR_LDS];
-  // counts[0..3]: K steps whose DMAs have landed, per DMA wave;
-  // counts[4..7]: K steps finished reading, per MFMA wave.
-  __shared__ __attribute__((aligned(16))) uint32_t counts[8];
+  // Progress counters, each written by one wave: [0, 4) K steps landed, per
+  // DMA wave; [4, 8) K steps read, per MFMA wave; [8, 12) tiles staged, per
+  // MFMA wave; [12, 20) tiles read from staging, per store wave.
+  __shared__ __attribute__((aligned(16))) uint32_t counts[20];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  if (tid < 8) counts[tid] = 0;
+  if (tid < 20) counts[tid] = 0;
   __syncthreads();
   const int ct = (int)(g.H * g.N / XR_T), mt = (int)(g.M / XR_T);
   const int ctile = (int)blockIdx.x % ct, rg = (int)blockIdx.x / ct;
@@ -400,6 +410,7 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
   char* const stg = lds + XR_EMAX + XR_RING * XR_EBLK;
   const int gq = lane >> 4, li = lane & 15;
   const uint32_t landed = lds_addr(&counts[0]), consumed = lds_addr(&counts[4]);
+  const uint32_t staged = lds_addr(&counts[8]), freed = lds_addr(&counts[12]);
 
   if (w < XR_MW) {
     // ---- MFMA waves: wave w owns latents 64 (w / 2) .. + 63 and tokens
@@ -416,11 +427,11 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
-    int slot = 0;
-    uint32_t seen = 0;
+    int slot = 0, tile = 0;
+    uint32_t seen = 0, seen_freed = 0;
     for (int j = 0, sk = 0; j < J; ++j) {
       // Step j (and, before step 0, the encoder chunk) has landed.
-      xr_wait_min4(landed, (uint32_t)(j + 1), seen);
+      xr_wait_min<4>(landed, (uint32_t)(j + 1), seen);
       mma_64x64_dsasm(reinterpret_cast<const bf16_t*>(E + sk * XR_EBLK),
                       reinterpret_cast<const bf16_t*>(ring + slot * XR_EBLK), lane, 64 * wm, 64 * wt, acc);
       // The fragment reads are complete (waited inside): the slot is free.
@@ -428,8 +439,8 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
       slot = slot == XR_RING - 1 ? 0 : slot + 1;
       if (++sk == nk) {
         sk = 0;
-        // Barrier G: the store waves have read the previous tile's staging.
-        asm volatile("s_barrier" ::: "memory");
+        // The store waves have read the previous tile's staging.
+        xr_wait_min<8>(freed, (uint32_t)tile, seen_freed);
         // The tile's act(x), f32, into the staging tile: block (mi, ni),
         // register r is latent 64 wm + 16 mi + 4 gq + r of token
         // 64 wt + 16 ni + li.
@@ -449,8 +460,9 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
             *reinterpret_cast<float4*>(stg + xr_stg(t, n)) = v;
             acc[mi][ni] = zero4();
           }
-        // Barrier F: the staging tile is written.
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // The staging writes are done (LDS order), then the tile is staged.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        xr_count_set(staged + 4 * w, (uint32_t)(++tile), lane);
       }
     }
     return;
@@ -477,22 +489,11 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
     const uint32_t cs0 = src(dw), cs1 = src(dw + XR_DW);
     const bf16_t* cg = g.a + (int64_t)rg * XR_T * g.D;
     const int64_t cstep = (int64_t)rg_count * XR_T * g.D;
-    // Tile barriers G and F: the MFMA waves reach tile i's once they have
-    // finished its last step, (i + 1) nk - 1.  This wave passes them in
-    // step j = (i + 1) nk + 2, right after learning that: until then the
-    // MFMA waves need no step it has not signalled (it signals step j - 1 in
-    // step j), and from step j + 1 on it waits for steps of tile i + 1.
-    int tiles_met = 0;
     int sk = 0, slot = 0;
     uint32_t seen = 0;
     for (int j = 0; j < J; ++j) {
       // Slot j % 3 held step j - 3: free once every MFMA wave has read it.
-      if (j >= XR_RING) xr_wait_min4(consumed, (uint32_t)(j - XR_RING + 1), seen);
-      if (tiles_met < ntile && j == (tiles_met + 1) * nk + 2) {
-        asm volatile("s_barrier" ::: "memory");  // G
-        asm volatile("s_barrier" ::: "memory");  // F
-        ++tiles_met;
-      }
+      if (j >= XR_RING) xr_wait_min<4>(consumed, (uint32_t)(j - XR_RING + 1), seen);
       const uint32_t d = lR + (uint32_t)(slot * XR_EBLK);
       dma16(cg, cs0 + (uint32_t)(sk * 64), d + (uint32_t)(dw * 1024));
       dma16(cg, cs1 + (uint32_t)(sk * 64), d + (uint32_t)((dw + XR_DW) * 1024));
@@ -510,10 +511,6 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     xr_count_set(landed + 4 * dw, (uint32_t)J, lane);  // step J - 1
-    for (; tiles_met < ntile; ++tiles_met) {
-      asm volatile("s_barrier" ::: "memory");  // G
-      asm volatile("s_barrier" ::: "memory");  // F
-    }
     return;
   }
 
@@ -554,12 +551,12 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
                                   reinterpret_cast<u32x4*>(g.q + o));
     }
   };
-  // Per tile: barriers G and F (as the MFMA waves), then the tile's pieces
-  // read from staging, formed and stored, before the next G.
+  // Per tile: once every MFMA wave has staged it, the tile's pieces are read
+  // from staging, formed and stored; then this wave's freed counter says so.
   int64_t row0 = (int64_t)rg * XR_T;  // first token row (b * T + t) of the tile
+  uint32_t seen = 0;
   for (int i = 0; i < ntile; ++i) {
-    asm volatile("s_barrier" ::: "memory");  // G
-    asm volatile("s_barrier" ::: "memory");  // F: the staging tile of tile i is written
+    xr_wait_min<4>(staged, (uint32_t)(i + 1), seen);
     // A tile lies inside one sequence (T % 128 == 0).
     const int64_t bb = row0 / g.T, t0 = row0 - bb * g.T;
     obase = ((bb * g.H + h) * g.T + t0) * g.N + n0 + 8 * li;
@@ -567,6 +564,9 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
     row0 += (int64_t)rg_count * XR_T;
 #pragma unroll
     for (int u = 0; u < XR_PC; ++u) store_piece(u);
+    // The pieces' staging reads are complete (their values went into the
+    // stores) and precede this write in LDS order.
+    xr_count_set(freed + 4 * sw, (uint32_t)(i + 1), lane);
   }
 }
 
