@@ -588,7 +588,14 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
 // decoder rows); x lands in the y buffer itself, in pairs of 32-latent
 // blocks as soon as the previous chunk's z steps have read them.  (A 4-slot ring, three
 // steps ahead in all 160 KiB of LDS, was slower: C5 1.08 against 0.98 ms
-// per launch.)
+// per launch.  So was a wave-role form like layer_x_roles_kernel, one
+// 512-thread workgroup per CU with 4 MFMA waves and 4 DMA waves handing a
+// 6-slot ring and the y buffer over through LDS counters: parity-green,
+// 816 against 780 us at C5.  A chunk took ~13.6 k cycles of an MFMA wave for
+// 4.1 k of MFMAs: the y epilogue ~2.4 k, fragment read latency and counter
+// polls every step; with one workgroup per CU no other workgroup's MFMAs
+// cover them, and the MFMA waves' 242 VGPRs leave no room to read the next
+// step's fragments early.)
 constexpr int YZ_C = T256 / 2;  // latents per chunk
 constexpr int YZ_RING = 3;
 constexpr int YZ_PREF = YZ_RING - 1;  // steps loaded ahead
