@@ -314,7 +314,11 @@ __global__ __launch_bounds__(NT, 2) void layer_gemm_kernel(LayerGemmArgs g) {
 // landed (vmcnt(0) there; 576 us with both); the landed counters read behind
 // each step's MFMAs for the next step (523 us: the DMA waves, one step
 // ahead, had rarely signalled it by then); 8 MFMA waves (64 x 32 blocks, two
-// a SIMD) with 4 store waves (535 us).
+// a SIMD) with 4 store waves (535 us).  Reading each step's fragments
+// behind the previous step's MFMAs needs a second fragment set: with 4
+// store waves (12 waves, 168 VGPRs) the MFMA waves spilled 157 registers,
+// among them fragment registers stored to scratch before their read had
+// completed (tests/asm_waits.py reports exactly that); not run.
 constexpr int XR_T = 128;                      // tile edge (tokens and latents)
 constexpr int XR_EBLK = XR_T * BK * 2;         // bytes of one 32-deep block of 128 rows
 constexpr int XR_EMAX = (T256 / BK) * XR_EBLK; // encoder chunk, D <= 256
