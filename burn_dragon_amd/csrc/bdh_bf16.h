@@ -238,6 +238,15 @@ __device__ __forceinline__ uint4 rope_cs4(float p, const float (&f)[4]) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 hipError_t launch_prefill_mfma(const PrefillArgs& a, bool rope, hipStream_t st);
+// Gram and state units of a one-interval RoPE call without decay or carried
+// state, T a multiple of 256, in 768-thread workgroups with wave roles
+// (roles_prefill.hip): PrefillArgs with n_iv = 1, gram_ids =
+// prefill_roles_gram_ids(S * ks, nb), state_units =
+// prefill_roles_state_units(S, N, Dp) or 0; partials as launch_prefill_mfma's.
+bool prefill_roles_fits(const PrefillArgs& a);
+int prefill_roles_gram_ids(int groups, int nb);
+int prefill_roles_state_units(int64_t S, int64_t N, int64_t Dp);
+hipError_t launch_prefill_roles(const PrefillArgs& a, hipStream_t st);
 // Workgroup ids a gram launch needs for `groups` groups of nb-block
 // intervals (ids are laid out so that one group's tiles share an XCD).
 int prefill_gram_ids(int groups, int nb);

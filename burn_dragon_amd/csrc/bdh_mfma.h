@@ -322,5 +322,33 @@ __device__ __forceinline__ void mma_64x128_frags(u32x4 (&af)[4], u32x4 (&bf)[8],
   mma_64x128_groups(af, bf, acc, between, std::make_integer_sequence<int, 8>{});
 }
 
+// Per-wave progress counters in LDS, each written by its one wave: a wave
+// waits until the least of a group's 4 counters (one 16-byte read at byte
+// address a) reaches target.  A poll, then a short sleep; bounded (about
+// 2^20 polls, tens of milliseconds), so it ends whatever happens; the
+// protocols that use it wait a few K steps at most.
+// seen: the least value this wave last read (counters only grow), so a wait
+// that an earlier poll already satisfied reads nothing.  N = 4 or 8
+// counters, 16-byte aligned.
+template <int N>
+__device__ __forceinline__ void wave_wait_min(uint32_t a, uint32_t target, uint32_t& seen) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  for (int poll = 0; poll < (1 << 20) && seen < target; ++poll) {
+    if (poll > 0) __builtin_amdgcn_s_sleep(1);
+    u32x4_t v, u = u32x4_t{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+    if (N == 8) {
+      asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                   : "=&v"(v), "=&v"(u) : "v"(a) : "memory");
+    } else {
+      asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+    }
+    const uint32_t m = min(min(min(v.x, v.y), min(v.z, v.w)), min(min(u.x, u.y), min(u.z, u.w)));
+    seen = (uint32_t)__builtin_amdgcn_readfirstlane((int)m);
+  }
+}
+__device__ __forceinline__ void wave_count_set(uint32_t a, uint32_t value, int lane) {
+  if (lane == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(value) : "memory");
+}
+
 }  // namespace mfma
 }  // namespace bdh

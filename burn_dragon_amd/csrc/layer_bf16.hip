@@ -366,34 +366,6 @@ __device__ __forceinline__ uint32_t xr_stg(int t, int n) {
   return (uint32_t)(t * 512 + ((((n >> 2) ^ (t & 15))) << 4) + 4 * (n & 3));
 }
 
-// Per-wave progress counters in LDS, each written by its one wave: a wave
-// waits until the least of a group's 4 counters (one 16-byte read at byte
-// address a) reaches target.  A poll, then a short sleep; bounded (about
-// 2^20 polls, tens of milliseconds), so it ends whatever happens; the
-// protocol's waits end within a few K steps.
-// seen: the least value this wave last read (counters only grow), so a wait
-// that an earlier poll already satisfied reads nothing.  N = 4 or 8
-// counters, 16-byte aligned.
-template <int N>
-__device__ __forceinline__ void xr_wait_min(uint32_t a, uint32_t target, uint32_t& seen) {
-  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-  for (int poll = 0; poll < (1 << 20) && seen < target; ++poll) {
-    if (poll > 0) __builtin_amdgcn_s_sleep(1);
-    u32x4_t v, u = u32x4_t{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
-    if (N == 8) {
-      asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
-                   : "=&v"(v), "=&v"(u) : "v"(a) : "memory");
-    } else {
-      asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
-    }
-    const uint32_t m = min(min(min(v.x, v.y), min(v.z, v.w)), min(min(u.x, u.y), min(u.z, u.w)));
-    seen = (uint32_t)__builtin_amdgcn_readfirstlane((int)m);
-  }
-}
-__device__ __forceinline__ void xr_count_set(uint32_t a, uint32_t value, int lane) {
-  if (lane == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(value) : "memory");
-}
-
 template <bool PLAIN>
 __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles_kernel(LayerGemmArgs g, int rg_count) {
   __shared__ __attribute__((aligned(16))) char lds[XR_LDS];
@@ -436,16 +408,16 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
     uint32_t seen = 0, seen_freed = 0;
     for (int j = 0, sk = 0; j < J; ++j) {
       // Step j (and, before step 0, the encoder chunk) has landed.
-      xr_wait_min<4>(landed, (uint32_t)(j + 1), seen);
+      wave_wait_min<4>(landed, (uint32_t)(j + 1), seen);
       mma_64x64_dsasm(reinterpret_cast<const bf16_t*>(E + sk * XR_EBLK),
                       reinterpret_cast<const bf16_t*>(ring + slot * XR_EBLK), lane, 64 * wm, 64 * wt, acc);
       // The fragment reads are complete (waited inside): the slot is free.
-      xr_count_set(consumed + 4 * w, (uint32_t)(j + 1), lane);
+      wave_count_set(consumed + 4 * w, (uint32_t)(j + 1), lane);
       slot = slot == XR_RING - 1 ? 0 : slot + 1;
       if (++sk == nk) {
         sk = 0;
         // The store waves have read the previous tile's staging.
-        xr_wait_min<8>(freed, (uint32_t)tile, seen_freed);
+        wave_wait_min<8>(freed, (uint32_t)tile, seen_freed);
         // The tile's act(x), f32, into the staging tile: block (mi, ni),
         // register r is latent 64 wm + 16 mi + 4 gq + r of token
         // 64 wt + 16 ni + li.
@@ -467,7 +439,7 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
           }
         // The staging writes are done (LDS order), then the tile is staged.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        xr_count_set(staged + 4 * w, (uint32_t)(++tile), lane);
+        wave_count_set(staged + 4 * w, (uint32_t)(++tile), lane);
       }
     }
     return;
@@ -498,7 +470,7 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
     uint32_t seen = 0;
     for (int j = 0; j < J; ++j) {
       // Slot j % 3 held step j - 3: free once every MFMA wave has read it.
-      if (j >= XR_RING) xr_wait_min<4>(consumed, (uint32_t)(j - XR_RING + 1), seen);
+      if (j >= XR_RING) wave_wait_min<4>(consumed, (uint32_t)(j - XR_RING + 1), seen);
       const uint32_t d = lR + (uint32_t)(slot * XR_EBLK);
       dma16(cg, cs0 + (uint32_t)(sk * 64), d + (uint32_t)(dw * 1024));
       dma16(cg, cs1 + (uint32_t)(sk * 64), d + (uint32_t)((dw + XR_DW) * 1024));
@@ -511,11 +483,11 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
       // landed once only step j's 2 DMAs are in flight.
       if (j > 0) {
         asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-        xr_count_set(landed + 4 * dw, (uint32_t)j, lane);
+        wave_count_set(landed + 4 * dw, (uint32_t)j, lane);
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    xr_count_set(landed + 4 * dw, (uint32_t)J, lane);  // step J - 1
+    wave_count_set(landed + 4 * dw, (uint32_t)J, lane);  // step J - 1
     return;
   }
 
@@ -561,7 +533,7 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
   int64_t row0 = (int64_t)rg * XR_T;  // first token row (b * T + t) of the tile
   uint32_t seen = 0;
   for (int i = 0; i < ntile; ++i) {
-    xr_wait_min<4>(staged, (uint32_t)(i + 1), seen);
+    wave_wait_min<4>(staged, (uint32_t)(i + 1), seen);
     // A tile lies inside one sequence (T % 128 == 0).
     const int64_t bb = row0 / g.T, t0 = row0 - bb * g.T;
     obase = ((bb * g.H + h) * g.T + t0) * g.N + n0 + 8 * li;
@@ -571,7 +543,7 @@ __global__ __launch_bounds__(64 * (XR_MW + XR_DW + XR_SW), 1) void layer_x_roles
     for (int u = 0; u < XR_PC; ++u) store_piece(u);
     // The pieces' staging reads are complete (their values went into the
     // stores) and precede this write in LDS order.
-    xr_count_set(freed + 4 * sw, (uint32_t)(i + 1), lane);
+    wave_count_set(freed + 4 * sw, (uint32_t)(i + 1), lane);
   }
 }
 

@@ -533,6 +533,68 @@ bdh_status run_gram_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, 
   if (launches) *launches += 3;
   return BDH_OK;
 }
+
+// The wave-role launch is parity-green but not yet faster at C2 (kernel
+// 259-283 us against 249-278 us for the 4-wave launch on the same boxes: its
+// one producer wave per SIMD takes ~2700 cycles to rotate an off-diagonal
+// tile's step, which the MFMA waves multiply in ~1050), so it stays off.
+constexpr bool kRolesPrefill = false;
+
+// One interval with RoPE, no decay and no carried state, T a multiple of
+// 256: the wave-role launch of gram and state units (roles_prefill.hip),
+// then the context kernel.  N splits: the fewest for which an off-diagonal
+// gram unit stays within 85 % of the launch's work per CU, counted in
+// producer steps (off-diagonal gram 1.5, diagonal 1, state 1.1 plus 4 for
+// its rho write), with at least 16 steps per range.  Returns BDH_UNSUPPORTED (nothing launched) where the
+// launch does not apply.
+bdh_status run_roles_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, int64_t S, int64_t Tp,
+                          int64_t Dp, int64_t Lp, int nb, int nk) {
+  const int st_units = a.state ? prefill_roles_state_units(S, a.N, Dp) : 0;
+  const double gram = (double)S * nk * (nb * (nb - 1) / 2 * 1.5 + nb);
+  const double stw = (double)st_units * ((double)(a.T / 32) * 1.1 + 4.0);
+  const double per = (gram + stw) / (double)device_cus();
+  const double heavy = nb > 1 ? 1.5 : 1.0;
+  int ks = 1;
+  for (int cand = 1; cand <= 8 && nk % (2 * cand) == 0 && (cand == 1 || nk / cand >= 16); cand *= 2) {
+    ks = cand;
+    if (heavy * nk / cand <= 0.85 * per) break;
+  }
+  PrefillArgs p{};
+  p.x = a.x;
+  p.freqs = a.freqs;
+  p.pos0 = a.pos0;
+  p.fixed = a.fixed;
+  p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;
+  p.L = a.L; p.Lp = Lp; p.n_iv = 1;
+  p.ks = ks; p.nb = nb;
+  p.gram_groups = (int)(S * ks);
+  p.gram_ids = prefill_roles_gram_ids(p.gram_groups, nb);
+  p.Tp = Tp; p.Dp = Dp;
+  p.rho_out = a.rho_out;
+  p.st_t0 = 0; p.st_Lc = a.T;
+  p.state_units = st_units;
+  p.rho_stream = 1;
+  if (!prefill_roles_fits(p)) return BDH_UNSUPPORTED;
+
+  void *vt = nullptr, *part = nullptr;
+  bdh_status stt = scratch(st, SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
+  if (stt != BDH_OK) return stt;
+  stt = scratch(st, SLOT_SCORES, (size_t)(ks * S * Lp * Lp) * sizeof(float), &part);
+  if (stt != BDH_OK) return stt;
+  p.vt = (const bf16_t*)vt;
+  p.part = (float*)part;
+  hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, VT_TILE), cdiv(Dp, VT_TILE), (unsigned)(a.B * a.Hv)),
+                     dim3(256), 0, st, a.v, (bf16_t*)vt, a.T, a.D, Tp, Dp);
+  BDH_HIP_TRY(hipGetLastError());
+  const int kt = ktime_begin(BDH_KERNEL_PREFILL, st);
+  BDH_HIP_TRY(launch_prefill_roles(p, st));
+  ktime_end(kt, st);
+  CtxArgs c{(const bf16_t*)vt, (const float*)part, a.ctx, a.H, a.Hv, a.T, a.D, a.L, Lp, Tp, Dp, S,
+            1, 0, 1, (int)cdiv(a.T, CTX_ROWS), nullptr, 0, 0};
+  BDH_HIP_TRY(launch_ctx(c, ks, st));
+  if (launches) *launches += 3;
+  return BDH_OK;
+}
 }  // namespace
 
 bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) {
@@ -559,6 +621,11 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     return run_carry_path(a, st, launches, S, Tp, Dp, n_iv, Lp, nb, nk);
   if (!a.state && a.rho_in == nullptr && a.freqs == nullptr && a.decay == nullptr && n_iv == 1)
     return run_gram_path(a, st, launches, S, Tp, Dp, Lp, nb, nk);
+  if (kRolesPrefill && n_iv == 1 && a.freqs != nullptr && a.decay == nullptr && a.rho_in == nullptr &&
+      a.T % T256 == 0) {
+    const bdh_status r = run_roles_path(a, st, launches, S, Tp, Dp, Lp, nb, nk);
+    if (r != BDH_UNSUPPORTED) return r;
+  }
 
   // N splits of the gram: the fewest for which the longest gram unit stays
   // within ~85% of the first launch's average work per workgroup slot (two
