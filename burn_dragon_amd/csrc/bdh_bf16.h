@@ -146,7 +146,8 @@ struct PrefillArgs {
   const float* decay;   // [H] or null
   int64_t H, Hv, T, N, D, S;
   // gram units
-  float* part;          // [KS, S, n_iv, Lp, Lp]
+  float* part;          // [KS, S, n_iv, Lp, Lp] (bf16 with part16, snap_wide_kernel only)
+  int part16;
   int64_t L, Lp, n_iv;
   int ks, nb;           // N splits (N/32 a multiple of 4 ks); 256-row blocks per interval
   int gram_groups;      // S * ks * n_iv

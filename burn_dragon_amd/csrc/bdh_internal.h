@@ -92,6 +92,9 @@ struct F32Args {
   float* part;          // scratch for the GEMMs' split-K partials (f32_path_part_elems floats)
   int64_t B, H, Hv, T, N, D, Lmax;
   bool state;           // false: context only (single interval, no rho)
+  // Context-only calls on pre-rotated queries: gram partials in bf16 (half
+  // the partial traffic; the scores then carry ~9 significant bits).
+  bool part16 = false;
 };
 size_t f32_path_part_elems(const F32Args& a);
 hipError_t run_f32_path(const F32Args& a, hipStream_t st, uint64_t* launches);
@@ -110,6 +113,9 @@ struct Bf16Args {
   int64_t B, H, Hv, T, N, D;
   int64_t L;            // state-carry interval (multiple of 128)
   bool state;           // false: context only (single interval, no rho)
+  // Context-only calls on pre-rotated queries: gram partials in bf16 (half
+  // the partial traffic; the scores then carry ~9 significant bits).
+  bool part16 = false;
 };
 bool bf16_shape_supported(int64_t N, int64_t D, const char** why);
 bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches);

@@ -1385,6 +1385,7 @@ bdh_status run_layer(const LayerArgs& a, hipStream_t st, uint64_t* launches) {
     b.B = a.B; b.H = a.H; b.Hv = 1; b.T = a.T; b.N = a.N; b.D = a.D;
     b.state = rho_out != nullptr;
     b.L = b.state ? a.state_interval : ((a.T + 127) / 128) * 128;
+    b.part16 = true;
     s = run_bf16_path(b, st, &n_attn);
     if (s != BDH_OK) return s;
   }

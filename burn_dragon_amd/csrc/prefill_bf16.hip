@@ -18,6 +18,8 @@
 // RoPE is applied to Q tiles between HBM and LDS, each lane computing the
 // (cos, sin) of its pairs from the f32 phase; with one interval rotated
 // queries are never written to memory.
+#include <type_traits>
+
 #include "bdh_bf16.h"
 
 namespace bdh {
@@ -48,13 +50,14 @@ struct CtxArgs {
   const float* rd;
   int rd_kr;
   int64_t rd_iv0;
+  int part16;            // part holds bf16 partials (snap_wide_kernel's part16)
 };
 
 // Workgroup id -> (row block, interval, stream): row blocks heaviest first
 // (row block rb contracts over 64 (rb + 1) columns), then interval, then
 // stream.  blockIdx.y is the column block: 4 waves x WC columns (WC = 64, or
 // 32 when the wide blocks would leave CUs with fewer than two workgroups).
-template <int KS, int WC>
+template <int KS, int WC, bool P16>
 __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
   constexpr int NI = WC / 32, COLS = 4 * WC;
   const int nz = (int)(a.S * a.n_ivc);
@@ -90,10 +93,20 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
   // column test).
   const int sm = tid >> 3, sc = tid & 7;
   const int dv = tid >> 2, kc = tid & 3;
+  // bf16 partials stay packed (two words per 4 scores) until they are summed.
   struct Stage {
-    float4 p[2][KS];
+    std::conditional_t<P16, uint2, float4> p[2][KS];
     uint4 v[NI * 2];
   } st;
+  auto score4 = [&](int i, int kp) -> float4 {
+    if constexpr (P16) {
+      const uint2 w = st.p[i][kp];
+      return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+    } else {
+      return st.p[i][kp];
+    }
+  };
+  const bf16_t* P16b = reinterpret_cast<const bf16_t*>(a.part) + (s * a.n_iv + iv) * a.Lp * a.Lp;
   auto load = [&](int kt) {
     const int64_t k0 = (int64_t)kt * CK;
 #pragma unroll
@@ -101,9 +114,13 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
       const int64_t row = r0 + sm + 32 * i, col = k0 + sc * 4;
       const bool in = row < Lc && col < kend;
 #pragma unroll
-      for (int kp = 0; kp < KS; ++kp)
-        st.p[i][kp] = in ? *reinterpret_cast<const float4*>(P0 + kp * pstride + row * a.Lp + col)
-                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int kp = 0; kp < KS; ++kp) {
+        if constexpr (P16)
+          st.p[i][kp] = in ? *reinterpret_cast<const uint2*>(P16b + kp * pstride + row * a.Lp + col) : make_uint2(0, 0);
+        else
+          st.p[i][kp] = in ? *reinterpret_cast<const float4*>(P0 + kp * pstride + row * a.Lp + col)
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     }
 #pragma unroll
     for (int i = 0; i < NI * 2; ++i) st.v[i] = ldg16(VT + (k0 >> 5) * (a.Dp * 32) + (e0 + dv + 64 * i) * 32 + kc * 8);
@@ -112,13 +129,14 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
     const int64_t k0 = (int64_t)kt * CK;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      float4 sv = st.p[i][0];
+      float4 sv = score4(i, 0);
 #pragma unroll
       for (int kp = 1; kp < KS; ++kp) {
-        sv.x += st.p[i][kp].x;
-        sv.y += st.p[i][kp].y;
-        sv.z += st.p[i][kp].z;
-        sv.w += st.p[i][kp].w;
+        const float4 pv = score4(i, kp);
+        sv.x += pv.x;
+        sv.y += pv.y;
+        sv.z += pv.z;
+        sv.w += pv.w;
       }
       // a step that runs past kend (ragged interval) reads zeros there
       const int64_t col = k0 + sc * 4;
@@ -211,15 +229,15 @@ __global__ __launch_bounds__(256, 2) void ctx_kernel(CtxArgs a) {
       }
 }
 
-template <int WC>
+template <int WC, bool P16>
 hipError_t launch_ctx_wc(const CtxArgs& c, int ks, hipStream_t st) {
   const int cols = 4 * WC;
   const dim3 grid((unsigned)(c.nrb * c.S * c.n_ivc), (unsigned)((c.D + cols - 1) / cols));
   switch (ks) {
-    case 1: hipLaunchKernelGGL((ctx_kernel<1, WC>), grid, dim3(256), 0, st, c); break;
-    case 2: hipLaunchKernelGGL((ctx_kernel<2, WC>), grid, dim3(256), 0, st, c); break;
-    case 4: hipLaunchKernelGGL((ctx_kernel<4, WC>), grid, dim3(256), 0, st, c); break;
-    case 8: hipLaunchKernelGGL((ctx_kernel<8, WC>), grid, dim3(256), 0, st, c); break;
+    case 1: hipLaunchKernelGGL((ctx_kernel<1, WC, P16>), grid, dim3(256), 0, st, c); break;
+    case 2: hipLaunchKernelGGL((ctx_kernel<2, WC, P16>), grid, dim3(256), 0, st, c); break;
+    case 4: hipLaunchKernelGGL((ctx_kernel<4, WC, P16>), grid, dim3(256), 0, st, c); break;
+    case 8: hipLaunchKernelGGL((ctx_kernel<8, WC, P16>), grid, dim3(256), 0, st, c); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -229,8 +247,12 @@ hipError_t launch_ctx_wc(const CtxArgs& c, int ks, hipStream_t st) {
 // and C5 (512 and more wide workgroups) narrow is slower.
 hipError_t launch_ctx(const CtxArgs& c, int ks, hipStream_t st) {
   const int64_t wide = c.nrb * c.S * c.n_ivc * ((c.D + CTX_COLS - 1) / CTX_COLS);
-  if (wide < 2 * (int64_t)device_cus()) return launch_ctx_wc<32>(c, ks, st);
-  return launch_ctx_wc<64>(c, ks, st);
+  if (c.part16) {
+    if (wide < 2 * (int64_t)device_cus()) return launch_ctx_wc<32, true>(c, ks, st);
+    return launch_ctx_wc<64, true>(c, ks, st);
+  }
+  if (wide < 2 * (int64_t)device_cus()) return launch_ctx_wc<32, false>(c, ks, st);
+  return launch_ctx_wc<64, false>(c, ks, st);
 }
 
 // ctx[s, t0 + t, :] += sum over the rd_kr readout partials (fixed order),
@@ -504,7 +526,8 @@ bdh_status run_gram_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, 
   void *vt = nullptr, *part = nullptr;
   bdh_status stt = scratch(st, SLOT_VT, (size_t)(a.B * a.Hv * Dp * Tp) * sizeof(bf16_t), &vt);
   if (stt != BDH_OK) return stt;
-  stt = scratch(st, SLOT_SCORES, (size_t)(ks * S * Lp * Lp) * sizeof(float), &part);
+  const size_t pbytes = a.part16 ? sizeof(bf16_t) : sizeof(float);
+  stt = scratch(st, SLOT_SCORES, (size_t)(ks * S * Lp * Lp) * pbytes, &part);
   if (stt != BDH_OK) return stt;
 
   hipLaunchKernelGGL(transpose_v_kernel, dim3(cdiv(Tp, VT_TILE), cdiv(Dp, VT_TILE), (unsigned)(a.B * a.Hv)),
@@ -512,6 +535,7 @@ bdh_status run_gram_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, 
   BDH_HIP_TRY(hipGetLastError());
 
   PrefillArgs p{};
+  p.part16 = a.part16 ? 1 : 0;
   p.x = a.x;
   p.H = a.H; p.Hv = a.Hv; p.T = a.T; p.N = a.N; p.D = a.D; p.S = S;
   p.part = (float*)part;
@@ -528,16 +552,19 @@ bdh_status run_gram_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, 
 
   const int64_t Lc0 = a.T < L ? a.T : L;
   CtxArgs cx{(const bf16_t*)vt, (const float*)part, a.ctx, a.H, a.Hv, a.T, a.D, L, Lp, Tp, Dp, S,
-             1, 0, 1, (int)cdiv(Lc0, CTX_ROWS), nullptr, 0, 0};
+             1, 0, 1, (int)cdiv(Lc0, CTX_ROWS), nullptr, 0, 0, p.part16};
   BDH_HIP_TRY(launch_ctx(cx, ks, st));
   if (launches) *launches += 3;
   return BDH_OK;
 }
 
-// The wave-role launch is parity-green but not yet faster at C2 (kernel
-// 259-283 us against 249-278 us for the 4-wave launch on the same boxes: its
-// one producer wave per SIMD takes ~2700 cycles to rotate an off-diagonal
-// tile's step, which the MFMA waves multiply in ~1050), so it stays off.
+// The wave-role launch is parity-green but no faster at C2, so it stays off:
+// with two N splits it takes 270 us against 270-274 us for the 4-wave launch
+// on the same box (four splits: 279-283 us).  One workgroup per CU gives up
+// what two 4-wave workgroups per CU have, a gram unit's rotation overlapping
+// a state unit's memory stream on the same CU; and the one producer wave per
+// SIMD needs ~2400 cycles (37 VALU instructions a row group) to rotate an
+// off-diagonal tile's step, which the MFMA waves multiply in ~1050.
 constexpr bool kRolesPrefill = false;
 
 // One interval with RoPE, no decay and no carried state, T a multiple of

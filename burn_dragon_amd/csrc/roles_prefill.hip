@@ -38,11 +38,11 @@ constexpr int RP_MW = 8;                    // MFMA waves
 constexpr int RP_PW = 4;                    // producer waves
 constexpr int RP_NT = 64 * (RP_MW + RP_PW);
 constexpr int RP_STAGE = 2 * T256 * BK * 2; // bytes of one stage: 512 rows of 32 bf16 (A 0..255, B 256..511)
-constexpr int RP_RAW = RP_STAGE;            // raw x of one step: 8 chunks x 16 B per producer lane
-constexpr int RP_FQ = RP_PW * 256;          // frequencies of one step (256 bytes a producer wave)
+constexpr int RP_RING = 3;                  // stages
+constexpr int RP_RAW = T256 * BK * 2;       // a state unit's raw x of one step: 4 chunks x 16 B per producer lane
 constexpr int RP_EP = 132;                  // epilogue staging row pitch (floats)
-constexpr int RP_LDS = 2 * RP_STAGE + 2 * RP_RAW + 2 * RP_FQ;
-static_assert(RP_MW * 16 * RP_EP * 4 <= 2 * RP_STAGE + 2 * RP_RAW, "epilogue staging fits the ring and slots");
+constexpr int RP_LDS = RP_RING * RP_STAGE + 2 * RP_RAW;
+static_assert(RP_MW * 16 * RP_EP * 4 <= RP_RING * RP_STAGE, "epilogue staging fits the ring");
 static_assert(RP_MW == 8 && RP_PW == 4, "the progress counters are read 8 and 4 at a time");
 
 enum { RK_DIAG = 0, RK_OFF = 1, RK_STATE = 2 };
@@ -94,7 +94,7 @@ __device__ __forceinline__ void roles_multiply(char* lds, uint32_t landed, uint3
     // The fragment reads have returned: the stage may be rewritten.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wave_count_set(consumed + 4 * w, (uint32_t)(j + 1), lane);
-    slot ^= 1;
+    slot = slot == RP_RING - 1 ? 0 : slot + 1;
   }
   // Every MFMA wave has read every stage, and the producers' last direct
   // loads (J + 1) have landed: the ring and the slots are free.
@@ -119,89 +119,64 @@ __device__ __forceinline__ void roles_multiply(char* lds, uint32_t landed, uint3
 }
 
 // Producer wave of a gram unit: A rows r0 .. r0 + 255, B rows r1 .. (off
-// diagonal; a diagonal tile's B rows are its A rows), N steps [kb, ke), an
-// even count.  Lane (kc = lane & 3, rr = 16 p + lane / 4) owns chunk kc of
-// row rr of each 64-row group g (g < 4: A rows, g >= 4: B rows): its raw x
-// arrives two steps ahead in its own 16 bytes of the raw slot, so only waits
-// order the slot (no barrier).  The (cos, sin) words: the first group of each
-// operand from frac(pos f), the next ones advanced by e(64 f), as the 4-wave
-// gram tiles compute them.
-// One wave does a SIMD's share of the rotation, so its waits are spread:
-// the refill of a slot (step j + 2) is issued one group at a time between
-// the rotations, the next step's slot is read halfway through the step, and
-// one LDS wait per step covers that read and the stage writes.
+// diagonal; a diagonal tile's B rows are its A rows), N steps [kb, ke).
+// Lane (kc = lane & 3, rr = 16 p + lane / 4) owns chunk kc of row rr of each
+// 64-row group g (g < 4: A rows, g >= 4: B rows).  Its raw x chunks and the
+// step's 4 pair frequencies are loaded into registers two steps ahead (three
+// register sets; the compiler places the waits), so the only LDS traffic a
+// step adds to the MFMA waves' fragment reads is its stage writes.  The
+// (cos, sin) words: the first group of each operand from frac(pos f), the
+// next ones advanced by e(64 f), as the 4-wave gram tiles compute them.
 template <int KIND>
 __device__ __forceinline__ void roles_produce_gram(const PrefillArgs& a, char* lds, uint32_t landed,
                                                    uint32_t consumed, int64_t s, int kb, int ke, int64_t r0,
                                                    int64_t r1) {
-  constexpr int NG = KIND == RK_OFF ? 8 : 4, NH = NG / 2;
+  constexpr int NG = KIND == RK_OFF ? 8 : 4;
   const int lane = threadIdx.x & 63, p = wave_id() - RP_MW;
   const int kc = lane & 3, rr = 16 * p + (lane >> 2);
   const int64_t rowb = a.N * 2;
   const char* X = reinterpret_cast<const char*>(a.x + s * a.T * a.N);
   const uint32_t voff = (uint32_t)((lane >> 2) * rowb + kc * 16);
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-  const uint32_t raw0 = lds0 + 2 * RP_STAGE, fq0 = raw0 + 2 * RP_RAW;
-  const char* raw_l = lds + 2 * RP_STAGE + p * 1024 + 16 * lane;            // + slot * RP_RAW + g * 4096
-  const char* fq_l = lds + 2 * RP_STAGE + 2 * RP_RAW + p * 256 + 16 * kc;  // + slot * RP_FQ
   auto gtok = [&](int g) -> int64_t { return (g < 4 ? r0 + 64 * g : r1 + 64 * (g - 4)) + 16 * p; };
-  // Group g's raw chunks of step kt, and the step's 16 pair frequencies
-  // (lane l: the even neuron 32 kt + 2 (l & 15); lanes 4 kc .. 4 kc + 3 are
-  // this lane's pairs).
-  auto dma_g = [&](int kt, int sl, int g) {
-    dma16(X + gtok(g) * rowb + (int64_t)kt * 64, voff, raw0 + (uint32_t)(sl * RP_RAW + (g * 4 + p) * 1024));
-  };
-  auto dma_f = [&](int kt, int sl) {
-    dma4(a.freqs + (int64_t)kt * BK, (uint32_t)(8 * (lane & 15)), fq0 + (uint32_t)(sl * RP_FQ + p * 256));
-  };
   struct Raw {
     uint4 x[NG];
-    float4 f;
+    float f[4];
   };
-  auto read_raw = [&](Raw& r, int sl) {
+  // Step kt's raw chunks and the frequencies of its pairs 16 kt + 4 kc ..
+  // (the even neurons 32 kt + 8 kc + 2 q).
+  auto load = [&](Raw& r, int kt) {
 #pragma unroll
-    for (int g = 0; g < NG; ++g) r.x[g] = *reinterpret_cast<const uint4*>(raw_l + sl * RP_RAW + g * 4096);
-    r.f = *reinterpret_cast<const float4*>(fq_l + sl * RP_FQ);
+    for (int g = 0; g < NG; ++g) r.x[g] = ldg16_off(X + gtok(g) * rowb + (int64_t)kt * 64, voff);
+    const float* fp = a.freqs + (int64_t)kt * BK + 8 * kc;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r.f[q] = fp[2 * q];
   };
   const float pA = rope_pos(a, r0 + rr), pB = rope_pos(a, r1 + rr);
   const float dstep = a.fixed ? 0.0f : 64.0f;
   const int J = ke - kb;
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no compiler-visible load left in flight
-  const int k1 = kb + 1 < ke ? kb + 1 : ke - 1;
-  dma_f(kb, 0);
-#pragma unroll
-  for (int g = 0; g < NG; ++g) dma_g(kb, 0, g);
-  dma_f(k1, 1);
-#pragma unroll
-  for (int g = 0; g < NG; ++g) dma_g(k1, 1, g);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NG + 1) : "memory");  // step kb landed
-  Raw ra, rb;
-  read_raw(ra, 0);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   uint32_t seen = 0;
-  // Step j from cur (its raw slot j & 1 already read); nxt receives step j + 1.
-  auto step = [&](int j, const Raw& cur, Raw& nxt) {
-    const int sl = j & 1;
+  int slot = 0;
+  // Step j from cur; the loads of step j + 2 go to nxt2 first.
+  auto step = [&](int j, const Raw& cur, Raw& nxt2) {
     const int kn = kb + j + 2 < ke ? kb + j + 2 : ke - 1;  // past the end the last step again (unused)
-    dma_f(kn, sl);
-    const float fq[4] = {cur.f.x, cur.f.y, cur.f.z, cur.f.w};
+    load(nxt2, kn);
     float ec[4], es[4], c[4], sn[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float fe = rope_frac(dstep, fq[q]);
+      const float fe = rope_frac(dstep, cur.f[q]);
       ec[q] = __builtin_amdgcn_cosf(fe);
       es[q] = __builtin_amdgcn_sinf(fe);
     }
-    // The stage of step j held step j - 2: every MFMA wave has read it.
-    if (j >= 2) wave_wait_min<8>(consumed, (uint32_t)(j - 1), seen);
-    bf16_t* stg = reinterpret_cast<bf16_t*>(lds + sl * RP_STAGE);
+    // The stage of step j held step j - RP_RING: every MFMA wave has read it.
+    if (j >= RP_RING) wave_wait_min<8>(consumed, (uint32_t)(j - RP_RING + 1), seen);
+    bf16_t* stg = reinterpret_cast<bf16_t*>(lds + slot * RP_STAGE);
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       if (g == 0 || g == 4) {
         const float pos = g == 0 ? pA : pB;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float fr = rope_frac(pos, fq[q]);
+          const float fr = rope_frac(pos, cur.f[q]);
           c[q] = __builtin_amdgcn_cosf(fr);
           sn[q] = __builtin_amdgcn_sinf(fr);
         }
@@ -218,24 +193,25 @@ __device__ __forceinline__ void roles_produce_gram(const PrefillArgs& a, char* l
                                   pack_bf16x2(c[3], sn[3]));
       const int row = (g < 4 ? 0 : T256) + 64 * (g & 3) + rr;
       *reinterpret_cast<uint4*>(&stg[lds_off(row, kc)]) = rot8_bf16(cur.x[g], cs);
-      dma_g(kn, sl, g);
-      if (g == NH - 1) {
-        // Step j + 1's loads (issued during step j - 1) have landed once only
-        // the NH + 1 issued so far in this step are in flight.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NH + 1) : "memory");
-        read_raw(nxt, sl ^ 1);
-      }
     }
-    // The stage writes (and the next step's slot reads) are done.
+    // The stage writes are done.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wave_count_set(landed + 4 * p, (uint32_t)(j + 1), lane);
+    slot = slot == RP_RING - 1 ? 0 : slot + 1;
   };
-  for (int j = 0; j < J; j += 2) {
-    step(j, ra, rb);
+  Raw ra, rb, rc;
+  load(ra, kb);
+  load(rb, kb + 1 < ke ? kb + 1 : ke - 1);
+  // Whole rounds of the three sets without branches (so that the compiler's
+  // waits inside the loop count exactly the loads in flight), then the rest.
+  int j = 0;
+  for (; j + 3 <= J; j += 3) {
+    step(j, ra, rc);
     step(j + 1, rb, ra);
+    step(j + 2, rc, rb);
   }
-  // The unused direct loads land before the MFMA waves reuse the slots.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (j < J) step(j, ra, rc);
+  if (j + 1 < J) step(j + 1, rb, ra);
   wave_count_set(landed + 4 * p, (uint32_t)(J + 1), lane);
 }
 
@@ -255,8 +231,8 @@ __device__ __forceinline__ void roles_produce_state(const PrefillArgs& a, char* 
   const char* VT = reinterpret_cast<const char*>(a.vt + (b * a.Hv + (a.Hv == 1 ? 0 : h)) * a.Dp * a.Tp);
   const int64_t vstep = a.Dp * 64;  // bytes of one 32-token step of v^T
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-  const uint32_t raw0 = lds0 + 2 * RP_STAGE;
-  const char* raw_l = lds + 2 * RP_STAGE + p * 1024 + 16 * lane;  // + slot * RP_RAW + c * 4096
+  const uint32_t raw0 = lds0 + RP_RING * RP_STAGE;
+  const char* raw_l = lds + RP_RING * RP_STAGE + p * 1024 + 16 * lane;  // + slot * RP_RAW + c * 4096
   // Chunk c = 2 hh + i: token 2 tp + i, neurons n0 + 128 hh + 8 oc .. + 7.
   const uint32_t xoff0 = (uint32_t)((2 * tp) * rowb + 16 * (lane >> 4));
   const uint32_t xoff1 = xoff0 + (uint32_t)rowb;
@@ -303,15 +279,15 @@ __device__ __forceinline__ void roles_produce_state(const PrefillArgs& a, char* 
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   uint32_t seen = 0;
   auto step = [&](int j, const Raw& cur, Raw& nxt) {
-    const int sl = j & 1;
-    // The stage of step j held step j - 2: every MFMA wave has read it.
-    if (j >= 2) wave_wait_min<8>(consumed, (uint32_t)(j - 1), seen);
-    issue_v(j, sl);
+    const int sl = j & 1, rs = j % RP_RING;
+    // The stage of step j held step j - RP_RING: every MFMA wave has read it.
+    if (j >= RP_RING) wave_wait_min<8>(consumed, (uint32_t)(j - RP_RING + 1), seen);
+    issue_v(j, rs);
     issue_x(j + 2 < J ? j + 2 : J - 1, sl);  // raw slot sl was read during step j - 1
     // Tokens of this step (positions exact in f32 below 2^24).
     const float p0 = a.fixed ? pbase : pbase + (float)(32 * j + 2 * tp);
     const float p1 = a.fixed ? pbase : p0 + 1.0f;
-    uint32_t* Aw = reinterpret_cast<uint32_t*>(lds + sl * RP_STAGE);
+    uint32_t* Aw = reinterpret_cast<uint32_t*>(lds + rs * RP_STAGE);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       float f0[8], f1[8];

@@ -206,6 +206,20 @@ __device__ __forceinline__ void snap_wide_unit(const PrefillArgs& a, bf16_t* lds
         for (int j = 0; j < 4; ++j)
           if (tj + j < ti) e[j] *= decay_pow_int(dk, l2d, (int)(ti - tj - j));
       }
+      if (a.part16) {
+        // bf16 partials (RNE): half the bytes written here and read by the
+        // context kernel.
+        bf16_t* dst = reinterpret_cast<bf16_t*>(a.part) + ((((int64_t)kp * a.S + s) * a.n_iv + iv) * a.Lp + ti) * a.Lp + tj;
+        if (tj + 3 < Lc) {
+          __builtin_nontemporal_store(u32x2{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3])},
+                                      reinterpret_cast<u32x2*>(dst));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (tj + j < Lc) dst[j] = (bf16_t)e[j];
+        }
+        return;
+      }
       float* dst = P + ti * a.Lp + tj;
       if (tj + 3 < Lc) {
         __builtin_nontemporal_store(floatx4{e[0], e[1], e[2], e[3]}, reinterpret_cast<floatx4*>(dst));

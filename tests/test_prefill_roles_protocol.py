@@ -1,11 +1,12 @@
 """CPU model of the hand-over protocol of prefill_roles_kernel (the one-interval
 RoPE prefill in wave roles, burn_dragon_amd/csrc/roles_prefill.hip): 8 MFMA
-waves and 4 producer waves of one workgroup, a 2-stage LDS ring of K steps,
-per-producer raw slots filled by direct loads two steps ahead (which land
-asynchronously, in issue order per wave) and read one step ahead, an
-epilogue whose staging overlaps the ring and the raw slots, and per-wave
-progress counters in LDS (steps
-written per producer, steps read per MFMA wave), no workgroup barriers.
+waves and 4 producer waves of one workgroup, a 3-stage LDS ring of K steps,
+an epilogue whose staging overlaps the ring, and per-wave progress counters
+in LDS (steps written per producer, steps read per MFMA wave), no workgroup
+barriers.  Gram producers load their raw rows into registers; state
+producers fill per-producer raw slots by direct loads two steps ahead
+(which land asynchronously, in issue order per wave) and read them one step
+ahead.
 A diagonal gram tile's MFMA waves 1 and 3 are inactive: they count steps as
 read without reading.  Random interleavings must always finish (no deadlock)
 and never let a wave read a stage that was already rewritten, nor let the
@@ -16,10 +17,10 @@ import random
 
 import pytest
 
-MW, PW, RING = 8, 4, 2
+MW, PW, RING = 8, 4, 3
 
 
-def _programs(J, inactive, wait_tail=True):
+def _programs(J, inactive, wait_tail=True, raw_slots=True):
     progs = []
     for w in range(MW):
         ops = []
@@ -35,13 +36,24 @@ def _programs(J, inactive, wait_tail=True):
             ops.append(("stage", w))
         progs.append(ops)
     for p in range(PW):
+        if not raw_slots:
+            # registers only: the loads never touch LDS
+            ops = []
+            for j in range(J):
+                if j >= RING:
+                    ops.append(("wait", "consumed", j - RING + 1))
+                ops.append(("write_slot", j % RING, j, p))
+                ops.append(("done", "landed", p, j + 1))
+            ops.append(("done", "landed", p, J + 1))
+            progs.append(ops)
+            continue
         ops = [("dma", p, 0, 0), ("dma", p, 1, min(1, J - 1)),
                ("dma_wait", p, 0), ("read_raw", p, 0, 0)]
         for j in range(J):
+            if j >= RING:
+                ops.append(("wait", "consumed", j - RING + 1))
             # raw slot j % 2 was read during step j - 1 (or before the loop)
             ops.append(("dma", p, j % 2, min(j + 2, J - 1)))
-            if j >= 2:
-                ops.append(("wait", "consumed", j - 1))
             ops.append(("write_slot", j % RING, j, p))
             ops.append(("dma_wait", p, j + 1))        # vmcnt: step j + 1's loads landed
             ops.append(("read_raw", p, (j + 1) % 2, min(j + 1, J - 1)))
@@ -55,11 +67,11 @@ def _programs(J, inactive, wait_tail=True):
 GROUP = {"landed": PW, "consumed": MW}
 
 
-def _run(J, inactive, seed, shared_counters=False, wait_tail=True):
+def _run(J, inactive, seed, shared_counters=False, wait_tail=True, raw_slots=True):
     """True if the waves finish with every read fresh, False on a deadlock;
     AssertionError on a stale read or a load landing in the staging."""
     rnd = random.Random(seed)
-    progs = _programs(J, inactive, wait_tail)
+    progs = _programs(J, inactive, wait_tail, raw_slots)
     n = len(progs)
     pc = [0] * n
     per_wave = {k: [0] * v for k, v in GROUP.items()}
@@ -132,9 +144,10 @@ def _run(J, inactive, seed, shared_counters=False, wait_tail=True):
 
 @pytest.mark.parametrize("J", [2, 3, 4, 5, 8])
 @pytest.mark.parametrize("inactive", [(), (1, 3)])
-def test_protocol_finishes_with_fresh_reads(J, inactive):
+@pytest.mark.parametrize("raw_slots", [True, False])
+def test_protocol_finishes_with_fresh_reads(J, inactive, raw_slots):
     for seed in range(40):
-        assert _run(J, inactive, seed), f"deadlock: {J} steps, inactive {inactive}, seed {seed}"
+        assert _run(J, inactive, seed, raw_slots=raw_slots), f"deadlock: {J} steps, inactive {inactive}, seed {seed}"
 
 
 def test_model_catches_shared_counters():
