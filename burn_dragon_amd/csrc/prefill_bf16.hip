@@ -18,6 +18,7 @@
 // RoPE is applied to Q tiles between HBM and LDS, each lane computing the
 // (cos, sin) of its pairs from the f32 phase; with one interval rotated
 // queries are never written to memory.
+#include <cstdlib>
 #include <type_traits>
 
 #include "bdh_bf16.h"
@@ -558,22 +559,27 @@ bdh_status run_gram_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, 
   return BDH_OK;
 }
 
-// The wave-role launch is parity-green but no faster at C2, so it stays off:
+// The wave-role launch is parity-green but no faster at C2, so it is off
+// unless BDH_PREFILL_ROLES=1 is set in the environment (read at each call):
 // with two N splits it takes 270 us against 270-274 us for the 4-wave launch
 // on the same box (four splits: 279-283 us).  One workgroup per CU gives up
 // what two 4-wave workgroups per CU have, a gram unit's rotation overlapping
 // a state unit's memory stream on the same CU; and the one producer wave per
 // SIMD needs ~2400 cycles (37 VALU instructions a row group) to rotate an
 // off-diagonal tile's step, which the MFMA waves multiply in ~1050.
-constexpr bool kRolesPrefill = false;
+bool roles_prefill_enabled() {
+  const char* e = getenv("BDH_PREFILL_ROLES");
+  return e != nullptr && e[0] == '1';
+}
 
 // One interval with RoPE, no decay and no carried state, T a multiple of
 // 256: the wave-role launch of gram and state units (roles_prefill.hip),
 // then the context kernel.  N splits: the fewest for which an off-diagonal
-// gram unit stays within 85 % of the launch's work per CU, counted in
-// producer steps (off-diagonal gram 1.5, diagonal 1, state 1.1 plus 4 for
-// its rho write), with at least 16 steps per range.  Returns BDH_UNSUPPORTED (nothing launched) where the
-// launch does not apply.
+// gram unit stays within the launch's work per CU, counted in producer
+// steps (off-diagonal gram 1.5, diagonal 1, state 1.1 plus 4 for its rho
+// write), with at least 16 steps per range (C2: 2, measured against 4 and
+// 8).  Returns BDH_UNSUPPORTED (nothing launched) where the launch does not
+// apply.
 bdh_status run_roles_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, int64_t S, int64_t Tp,
                           int64_t Dp, int64_t Lp, int nb, int nk) {
   const int st_units = a.state ? prefill_roles_state_units(S, a.N, Dp) : 0;
@@ -584,7 +590,7 @@ bdh_status run_roles_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
   int ks = 1;
   for (int cand = 1; cand <= 8 && nk % (2 * cand) == 0 && (cand == 1 || nk / cand >= 16); cand *= 2) {
     ks = cand;
-    if (heavy * nk / cand <= 0.85 * per) break;
+    if (heavy * nk / cand <= per) break;
   }
   PrefillArgs p{};
   p.x = a.x;
@@ -648,8 +654,8 @@ bdh_status run_bf16_path(const Bf16Args& a, hipStream_t st, uint64_t* launches) 
     return run_carry_path(a, st, launches, S, Tp, Dp, n_iv, Lp, nb, nk);
   if (!a.state && a.rho_in == nullptr && a.freqs == nullptr && a.decay == nullptr && n_iv == 1)
     return run_gram_path(a, st, launches, S, Tp, Dp, Lp, nb, nk);
-  if (kRolesPrefill && n_iv == 1 && a.freqs != nullptr && a.decay == nullptr && a.rho_in == nullptr &&
-      a.T % T256 == 0) {
+  if (n_iv == 1 && a.freqs != nullptr && a.decay == nullptr && a.rho_in == nullptr && a.T % T256 == 0 &&
+      roles_prefill_enabled()) {
     const bdh_status r = run_roles_path(a, st, launches, S, Tp, Dp, Lp, nb, nk);
     if (r != BDH_UNSUPPORTED) return r;
   }
