@@ -112,6 +112,27 @@ __device__ __forceinline__ void carry_loader(const CarryArgs& a, char* lds, int6
   const int tp = rtid & 15, nv = rtid >> 4;
   float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (ROPE) load_freq4(a.freqs + n0 + 8 * nv, fq);
+  // (cos, sin) of the lane's 4 pairs at its two tokens of the step rotated
+  // next: from frac(pos f) for step 0 (positions clamped to T - 1 as the
+  // rows are), then advanced by e(32 f) a step, one complex multiply a pair
+  // instead of a phase, a cosine and a sine (the steps run in order).
+  float ca[4], sa[4], cb[4], sb[4], ec[4], es[4];
+  if (ROPE) {
+    const int64_t ta = 2 * tp < a.T ? 2 * tp : a.T - 1, tb = 2 * tp + 1 < a.T ? 2 * tp + 1 : a.T - 1;
+    const float pa = (float)(a.fixed ? a.pos0 : a.pos0 + ta);
+    const float pb = (float)(a.fixed ? a.pos0 : a.pos0 + tb);
+    const float dstep = a.fixed ? 0.0f : (float)BK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float fa = rope_frac(pa, fq[j]), fb = rope_frac(pb, fq[j]), fe = rope_frac(dstep, fq[j]);
+      ca[j] = __builtin_amdgcn_cosf(fa);
+      sa[j] = __builtin_amdgcn_sinf(fa);
+      cb[j] = __builtin_amdgcn_cosf(fb);
+      sb[j] = __builtin_amdgcn_sinf(fb);
+      ec[j] = __builtin_amdgcn_cosf(fe);
+      es[j] = __builtin_amdgcn_sinf(fe);
+    }
+  }
   // q^T of step k (tokens 2 tp, 2 tp + 1 of neuron 8 nv + e) into buffer k & 1.
   const float dk = DECAY ? a.decay[h] : 1.0f;
   const float l2d = DECAY ? decay_log2(dk) : 0.0f;
@@ -133,14 +154,22 @@ __device__ __forceinline__ void carry_loader(const CarryArgs& a, char* lds, int6
     uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
     const int64_t t = (int64_t)kt * BK + 2 * tp;
     if (ROPE) {
-      // Tokens past T hold row T - 1 (see issue) and are rotated at its
-      // position, so their q is row T - 1's; their v^T columns are zero, so
-      // they add nothing to rho.  Sums of integers below 2^24 are exact in f32.
-      const int64_t ta = t < a.T ? t : a.T - 1, tb = t + 1 < a.T ? t + 1 : a.T - 1;
-      const float pa = (float)(a.fixed ? a.pos0 : a.pos0 + ta);
-      const float pb = (float)(a.fixed ? a.pos0 : a.pos0 + tb);
-      c0 = rope_cs4(pa, fq);
-      c1 = rope_cs4(pb, fq);
+      // Tokens past T hold row T - 1 (see issue) and are rotated at their
+      // own positions; their v^T columns are zero, so they add nothing to
+      // rho, and their q rows are not stored.
+      c0 = make_uint4(pack_bf16x2(ca[0], sa[0]), pack_bf16x2(ca[1], sa[1]), pack_bf16x2(ca[2], sa[2]),
+                      pack_bf16x2(ca[3], sa[3]));
+      c1 = make_uint4(pack_bf16x2(cb[0], sb[0]), pack_bf16x2(cb[1], sb[1]), pack_bf16x2(cb[2], sb[2]),
+                      pack_bf16x2(cb[3], sb[3]));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float na = ca[j] * ec[j] - sa[j] * es[j], ma = sa[j] * ec[j] + ca[j] * es[j];
+        const float nb = cb[j] * ec[j] - sb[j] * es[j], mb = sb[j] * ec[j] + cb[j] * es[j];
+        ca[j] = na;
+        sa[j] = ma;
+        cb[j] = nb;
+        sb[j] = mb;
+      }
     }
     uint4 u0, u1;  // the q^T source rows: rotated and, with decay, weighted
     if (DECAY) {
@@ -267,7 +296,7 @@ __device__ __forceinline__ void carry_mma(const CarryArgs& a, char* lds, int64_t
   // store instruction writes 4 whole 256-byte row pieces (the rotation
   // lanes' own layout would write 64-byte pieces, each 128-byte line then
   // completed by another wave later, which costs HBM write bytes).  Rows
-  // past T hold row T - 1's q and are stored there again (the same bytes).
+  // past T (row T - 1's x rotated at their own positions) are not stored.
   auto store_q = [&](int kt, int slot) {
     const char* R = lds + slot * CARRY_STAGE;
     const int c = lane & 15;
@@ -277,8 +306,8 @@ __device__ __forceinline__ void carry_mma(const CarryArgs& a, char* lds, int64_t
       const uint4 v = *reinterpret_cast<const uint4*>(R + r * 256 + ((c ^ (r & 15)) << 4));
       const int64_t t = (int64_t)kt * BK + r;
       // Read by the next launch after ~1 GB of other traffic: streaming stores.
-      __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w},
-                                  reinterpret_cast<u32x4*>(Q + (t < a.T ? t : a.T - 1) * a.N + n0 + 8 * c));
+      if (t < a.T)
+        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(Q + t * a.N + n0 + 8 * c));
     }
   };
 
