@@ -209,6 +209,14 @@ int prefill_carry_units(int64_t S, int64_t N, int64_t Dp);
 // tiles) it is the gram of a context-only call on pre-rotated queries.
 int snap_wide_ids(int groups, int nb, int rd_pg);
 hipError_t launch_snap_wide(const PrefillArgs& a, hipStream_t st);
+// Gram tiles of a context-only call (wide_gram.hip): PrefillArgs as for
+// snap_wide with rd_pg = 0, in 4-wave workgroups (a 128 x 128 block a wave);
+// wide_gram_fits says whether a's shape suits them (one interval, no decay,
+// pre-rotated queries, whole 256-row blocks, an even step count per N
+// range), gram_ids = wide_gram_ids(groups, nb).
+bool wide_gram_fits(const PrefillArgs& a);
+int wide_gram_ids(int groups, int nb);
+hipError_t launch_wide_gram(const PrefillArgs& a, hipStream_t st);
 hipError_t launch_prefill_carry(const CarryArgs& a, hipStream_t st);
 
 // RoPE position of token t of the call (attention.rs:488-501 with the

@@ -509,8 +509,12 @@ bdh_status run_carry_path(const Bf16Args& a, hipStream_t st, uint64_t* launches,
 }
 
 // Context only (no state, no carried state), queries already rotated, no
-// decay: v^T, the gram tiles in 8-wave workgroups (snap_wide.hip, the tiles
-// of the state-carry form without readouts), the context kernel.  N splits:
+// decay: v^T, the gram tiles, the context kernel.  The tiles run in 4-wave
+// workgroups of 128 x 128 blocks a wave (wide_gram.hip) where the shape
+// suits them (whole 256-row blocks, an even step count per N range), else in
+// 8-wave workgroups (snap_wide.hip, the tiles of the state-carry form without
+// readouts).  Measured at C5 (same box): 4-wave tiles 10.97-11.06 ms a
+// forward against 11.18-11.22 ms.  N splits:
 // the fewest of 1, 2 or 4 with the fewest steps in rounds of units over the
 // CUs.  (The layer's attention runs here: the layer rotates q in its GEMM
 // epilogue.)
@@ -547,8 +551,10 @@ bdh_status run_gram_path(const Bf16Args& a, hipStream_t st, uint64_t* launches, 
   p.gram_ids = snap_wide_ids(p.gram_groups, nb, 0);
   p.vt = (const bf16_t*)vt;
   p.Tp = Tp; p.Dp = Dp;
+  const bool wide = wide_gram_fits(p);
+  if (wide) p.gram_ids = wide_gram_ids(p.gram_groups, nb);
   const int kt = ktime_begin(BDH_KERNEL_PREFILL, st);
-  BDH_HIP_TRY(launch_snap_wide(p, st));
+  BDH_HIP_TRY(wide ? launch_wide_gram(p, st) : launch_snap_wide(p, st));
   ktime_end(kt, st);
 
   const int64_t Lc0 = a.T < L ? a.T : L;

@@ -19,7 +19,7 @@ CSRC = os.path.join(ROOT, "burn_dragon_amd", "csrc")
 # Translation units with assembly LDS reads (bdh_mfma.h: mma_64x128_dsasm,
 # mma_64x64_dsasm, frag_64x128_read; bdh_gemm_f32.h: dread_kc, dread_rc).
 UNITS = ["snap_wide.hip", "carry_prefill.hip", "layer_bf16.hip", "mfma_prefill.hip", "prefill_f32.hip", "vjp.hip",
-         "roles_prefill.hip"]
+         "roles_prefill.hip", "wide_gram.hip"]
 
 _HEAD = "kern:\n"
 
