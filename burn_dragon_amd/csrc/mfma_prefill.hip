@@ -52,7 +52,14 @@ __device__ __forceinline__ void gram_unit(const PrefillArgs& a, bf16_t* lds, int
   const int64_t rowb = a.N * 2;  // bytes per x row
   const char* X = reinterpret_cast<const char*>(a.x + (s * a.T + t0) * a.N);
   const int nk = (int)(a.N / BK);
-  const int kb = (int)((int64_t)nk * kp / a.ks), ke = (int)((int64_t)nk * (kp + 1) / a.ks);
+  // RoPE units: uniform step bounds (readfirstlane), so that the loop
+  // counter and the direct loads' addresses live in scalar registers (the
+  // other units' loops already keep them there, and are worse with it).
+  int kb = (int)((int64_t)nk * kp / a.ks), ke = (int)((int64_t)nk * (kp + 1) / a.ks);
+  if constexpr (ROPE) {
+    kb = __builtin_amdgcn_readfirstlane(kb);
+    ke = __builtin_amdgcn_readfirstlane(ke);
+  }
 
   // Loader: 4 lanes per 64-byte row segment; group g < 4 covers A rows
   // rb + 64 g, g = 4, 5 cover B rows rb + 64 (g - 4).  WHOLE tiles (inside
