@@ -79,6 +79,33 @@ __device__ __forceinline__ void mma128_frags(u32x4 (&af)[8], u32x4 (&bf)[8], flo
   mma128_groups(af, bf, acc, between, std::make_integer_sequence<int, 8>{});
 }
 
+// The block's scores through the wave's own 16 x 132-float slab of LDS
+// (rows 16 mi .. of the block at a time), emit(row, col, lo, hi) getting
+// columns col .. col + 7 of one row (col = 8 (lane & 15)), 4 rows a call.
+// The slab is the wave's alone and the ring is idle by then, so no
+// workgroup barrier: lgkmcnt waits order the wave's own writes and reads.
+template <class Emit>
+__device__ __forceinline__ void wave_epilogue8(const floatx4 (&acc)[8][8], bf16_t* lds, int w, int lane,
+                                               Emit&& emit) {
+  constexpr int EP = 132;
+  float* E = reinterpret_cast<float*>(lds) + w * 16 * EP;
+#pragma unroll
+  for (int mi = 0; mi < 8; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) E[acc16_row(lane, r) * EP + ni * 16 + acc16_col(lane)] = acc[mi][ni][r];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int rr = 0; rr < 16; rr += 4) {
+      const int row = rr + (lane >> 4), col = 8 * (lane & 15);
+      emit(mi * 16 + row, col, *reinterpret_cast<const float4*>(&E[row * EP + col]),
+           *reinterpret_cast<const float4*>(&E[row * EP + col + 4]));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
 // Tile of stream s, N range kp: A = token rows ri .. ri + 255, B = token rows
 // rj .. (off diagonal) or the A rows (diagonal).  Wave w fetches the 16-row
 // blocks w + 4 j of the stage (j < 4: A, j >= 4: B); the lane writing LDS
@@ -196,32 +223,26 @@ __device__ __forceinline__ void wide_gram_unit(const PrefillArgs& a, bf16_t* lds
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   dma_wait_barrier<0>();  // the epilogue reuses the ring
 
-  // Scores (ti, tj), 0 on and above the diagonal; the block's two 64-row
-  // halves through epilogue_64x128 (every wave takes part in its barriers).
+  // Scores (ti, tj), 0 on and above the diagonal.
   const int64_t Lp = a.Lp;
   const int64_t wr0 = ri + 128 * wr, wc0 = rj + 128 * wc;
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf) {
-    floatx4 half[4][8];
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < 8; ++ni) half[mi][ni] = acc[4 * hf + mi][ni];
-    epilogue_64x128(half, lds, w, lane, [&](int row, int col, float4 v) {
-      const int64_t ti = wr0 + 64 * hf + row, tj = wc0 + col;
-      if (!active) return;
-      const float e[4] = {tj < ti ? v.x : 0.0f, tj + 1 < ti ? v.y : 0.0f, tj + 2 < ti ? v.z : 0.0f,
-                          tj + 3 < ti ? v.w : 0.0f};
-      const int64_t o = (((int64_t)kp * a.S + s) * Lp + ti) * Lp + tj;
-      // Streaming stores: the partials are read once, by the context kernel.
-      if (a.part16) {
-        __builtin_nontemporal_store(u32x2{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3])},
-                                    reinterpret_cast<u32x2*>(reinterpret_cast<bf16_t*>(a.part) + o));
-      } else {
-        __builtin_nontemporal_store(floatx4{e[0], e[1], e[2], e[3]}, reinterpret_cast<floatx4*>(a.part + o));
-      }
-    });
-  }
+  if (!active) return;  // the idle wave of a diagonal tile writes nothing (no barrier follows)
+  wave_epilogue8(acc, lds, w, lane, [&](int row, int col, float4 lo, float4 hi) {
+    const int64_t ti = wr0 + row, tj = wc0 + col;
+    const float e[8] = {tj < ti ? lo.x : 0.0f,     tj + 1 < ti ? lo.y : 0.0f, tj + 2 < ti ? lo.z : 0.0f,
+                        tj + 3 < ti ? lo.w : 0.0f, tj + 4 < ti ? hi.x : 0.0f, tj + 5 < ti ? hi.y : 0.0f,
+                        tj + 6 < ti ? hi.z : 0.0f, tj + 7 < ti ? hi.w : 0.0f};
+    const int64_t o = (((int64_t)kp * a.S + s) * Lp + ti) * Lp + tj;
+    // Streaming stores: the partials are read once, by the context kernel.
+    if (a.part16) {
+      __builtin_nontemporal_store(u32x4{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3]), pack_bf16x2(e[4], e[5]),
+                                        pack_bf16x2(e[6], e[7])},
+                                  reinterpret_cast<u32x4*>(reinterpret_cast<bf16_t*>(a.part) + o));
+    } else {
+      __builtin_nontemporal_store(floatx4{e[0], e[1], e[2], e[3]}, reinterpret_cast<floatx4*>(a.part + o));
+      __builtin_nontemporal_store(floatx4{e[4], e[5], e[6], e[7]}, reinterpret_cast<floatx4*>(a.part + o + 4));
+    }
+  });
 }
 
 // Group g = (stream, N range); its units: the nb (nb - 1) / 2 off-diagonal
