@@ -54,7 +54,8 @@ def parse():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--decode-warmup", type=int, default=4)
     ap.add_argument("--decode-prefill", type=int, default=1024, help="tokens prefilled into rho")
-    ap.add_argument("--model-steps", type=int, default=2, help="timed C5 model forwards")
+    ap.add_argument("--model-steps", type=int, default=6, help="timed C5 model forwards")
+    ap.add_argument("--model-warmup", type=int, default=2, help="untimed C5 model forwards before them")
     ap.add_argument("--model-decode-steps", type=int, default=32,
                     help="timed C5 greedy decode steps")
     ap.add_argument("--only", choices=("all", "prefill", "decode", "long", "model", "model-decode",
@@ -512,7 +513,7 @@ def bench_model(torch, args):
     if w is None:
         raise RuntimeError("model weights unsupported")
     tokens = torch.randint(0, V, (B, T), generator=g, device=dev, dtype=torch.int32)
-    for _ in range(1):
+    for _ in range(max(1, args.model_warmup)):
         assert bd.model_forward_logits(tokens, w, position=0) is not None
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
@@ -531,7 +532,7 @@ def bench_model(torch, args):
     print(f"[model] {ms:.2f} ms/forward, {M / (ms * 1e-3) / 1e6:.2f} M tok/s, "
           f"{achieved:.1f} TFLOP/s", flush=True)
     return {"metric": "C5 6-layer BDH forward tokens/s", "value": M / (ms * 1e-3),
-            "unit": "tokens/s", "ms_per_forward": ms, "steps": steps,
+            "unit": "tokens/s", "ms_per_forward": ms, "steps": steps, "warmup": max(1, args.model_warmup),
             "config": {"workload": "C5 6-layer BDH forward, byte vocabulary: B16 T1024 D256 nh4 "
                                    "N8192, shared low-rank weights std 0.02, bf16 MFMA / fp32 acc, "
                                    "RoPE fused, random tokens"},
