@@ -31,6 +31,7 @@ def _case(rng, B, H, T, N, D):
     (2, 2, 256, 256, 64, 5, False),     # 4 latent chunks over 2 heads in one workgroup per token tile
     (1, 3, 512, 256, 192, 3, True),     # D = 192 (decoder rows past D clamped), 6 chunks over 3 heads
     (1, 4, 512, 512, 256, 0, True),     # D = 256, 16 chunks in 4 splits
+    (1, 2, 512, 512, 128, 4, False),    # context only on 4-wave gram tiles: an off-diagonal tile, 4 N ranges
 ])
 def test_layer_matches_oracle(oracle, B, H, T, N, D, pos, want_rho):
     torch = need_gpu()
